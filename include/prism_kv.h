@@ -1,0 +1,156 @@
+/*
+ * prism_kv.h -- C ABI of libprism_kv.so, the MI355X (gfx950) paged KV-cache hot path.
+ *
+ * The library replaces the GPU half of Prism's paged KV cache:
+ *   - the third-party op flash_attn.flash_attn_with_kvcache(q, k_cache, v_cache, k=, v=,
+ *     cache_seqlens=, block_table=, causal=True), which Prism calls at
+ *     engine/executor.py:119-120, :151-153, :260-261, :385-386 and
+ *     engine/speculative_executor.py:150-153 (append + paged attention in one call);
+ *   - the per-page torch copy_ loop of FlashAttnKVCache.transfer_sequence
+ *     (engine/kv_cache.py:189-207), generalised to copy-on-write and compaction.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensors are device pointers owned by the caller.  Nothing here allocates device
+ *     memory, synchronises the host, or touches global mutable state, so every call can be
+ *     captured in a HIP graph.  Work is enqueued on `stream` (a hipStream_t; NULL = default).
+ *   - K/V element type is bf16 (passed as raw 16-bit words).  A paged cache is laid out
+ *     [num_pages, page_size, n_kv, head_dim] with the last three dims contiguous
+ *     (engine/kv_cache.py:37-46); `*_page_stride` is the element distance between pages.
+ *   - Strides are in elements (16-bit words) unless the name says _bytes.  The innermost
+ *     (head_dim) dimension must be contiguous and every row 16-byte aligned.
+ *   - block_table is int32 [batch, bt_stride] (only the first max_blocks columns are read);
+ *     cache_seqlens is int32 [batch] and holds each sequence's length BEFORE the append
+ *     (engine/kv_cache.py:123-153).
+ *   - `status` (nullable) is a device int32 the kernels OR error bits into instead of
+ *     touching memory they must not: PKV_STATUS_BAD_PAGE when a block-table entry the call
+ *     needs lies outside [0, num_pages).  The host reads it when it chooses to.
+ *   - Return value: PKV_OK, or a negative PKV_E* code with a message in pkv_last_error()
+ *     (thread-local).  Argument checks run on the host before anything is launched.
+ */
+#ifndef PRISM_KV_H
+#define PRISM_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PKV_ABI_VERSION 1
+
+#define PKV_OK 0
+#define PKV_EINVAL (-1)  /* bad shape, stride, alignment or size */
+#define PKV_EHIP (-2)    /* a HIP runtime call or kernel launch failed */
+#define PKV_ENOSPC (-3)  /* workspace smaller than pkv_decode_workspace_bytes() */
+
+#define PKV_STATUS_BAD_PAGE 1
+
+/* ABI version of the loaded library (PKV_ABI_VERSION it was built with). */
+int pkv_abi_version(void);
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* pkv_last_error(void);
+
+/*
+ * Slot-mapped append (replaces the append half of flash_attn_with_kvcache(k=, v=)).
+ * For b < batch, j < s_new:  slot = cache_seqlens[b] + j,
+ *   k_cache[block_table[b, slot / page_size], slot % page_size] = k_new[b, j]   (same for v).
+ * Bit-exact 16-byte copies.  k_new/v_new are [batch, s_new, n_kv, head_dim] with the given
+ * batch/seq/head strides (Prism passes views into the fused QKV projection output).
+ */
+int pkv_append(const void* k_new, int64_t kn_sb, int64_t kn_ss, int64_t kn_sh,
+               const void* v_new, int64_t vn_sb, int64_t vn_ss, int64_t vn_sh,
+               void* k_cache, void* v_cache, int64_t cache_page_stride,
+               const int32_t* block_table, int64_t bt_stride, const int32_t* cache_seqlens,
+               int32_t batch, int32_t s_new, int32_t n_kv, int32_t head_dim,
+               int32_t page_size, int32_t num_pages, int32_t max_blocks,
+               int32_t* status, void* stream);
+
+/*
+ * Bytes of workspace pkv_decode_attn needs for these sizes (split-K partial outputs and
+ * log-sum-exp terms).  split_tokens = 0 asks for the library's own choice, exactly as
+ * pkv_decode_attn would make it.
+ */
+size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv,
+                                  int32_t head_dim, int32_t page_size, int32_t max_blocks,
+                                  int32_t split_tokens);
+
+/*
+ * Paged decode attention with GQA and split-K (flash_attn_with_kvcache with s_q small:
+ * decode, s_q = 1, engine/executor.py:151-153, :260-261, :385-386; speculative verify,
+ * s_q = k+1, engine/speculative_executor.py:150-153).  Needs s_q * (n_heads / n_kv) <= 64.
+ *
+ * If k_new/v_new are non-NULL they are appended at cache_seqlens[b] (as pkv_append) and the
+ * keys are [0, cache_seqlens[b] + s_q); otherwise the keys are [0, cache_seqlens[b]).
+ * Query j of sequence b (length L_b keys) attends to keys t <= L_b - s_q + j when causal
+ * (bottom-right aligned), to all L_b keys otherwise.  Query head h reads KV head
+ * h / (n_heads / n_kv).  Scores are scaled by softmax_scale (Prism uses the default
+ * 1/sqrt(head_dim)); softmax and accumulation are fp32, out is bf16 [batch, s_q, n_heads,
+ * head_dim] with the given strides.  A query row with no visible key gets zeros.
+ * split_tokens (multiple of 32, or 0 = library choice) is the KV range one workgroup reduces
+ * before the split-K combine.  workspace must hold pkv_decode_workspace_bytes() bytes.
+ */
+int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                    const void* k_new, int64_t kn_sb, int64_t kn_ss, int64_t kn_sh,
+                    const void* v_new, int64_t vn_sb, int64_t vn_ss, int64_t vn_sh,
+                    void* k_cache, void* v_cache, int64_t cache_page_stride,
+                    const int32_t* block_table, int64_t bt_stride, const int32_t* cache_seqlens,
+                    void* out, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+                    void* workspace, size_t workspace_bytes,
+                    int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv, int32_t head_dim,
+                    int32_t page_size, int32_t num_pages, int32_t max_blocks,
+                    int32_t causal, float softmax_scale, int32_t split_tokens,
+                    int32_t* status, void* stream);
+
+/*
+ * Varlen chunked-prefill attention over paged KV (flash_attn_with_kvcache with s_q = chunk,
+ * engine/executor.py:119-120), bf16 MFMA.  Same arguments and semantics as
+ * pkv_decode_attn without the split-K workspace; any s_q >= 1.  When k_new/v_new are given
+ * the chunk is appended first (pkv_append) and attention then reads it from the cache.
+ */
+int pkv_prefill_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                     const void* k_new, int64_t kn_sb, int64_t kn_ss, int64_t kn_sh,
+                     const void* v_new, int64_t vn_sb, int64_t vn_ss, int64_t vn_sh,
+                     void* k_cache, void* v_cache, int64_t cache_page_stride,
+                     const int32_t* block_table, int64_t bt_stride, const int32_t* cache_seqlens,
+                     void* out, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+                     int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv, int32_t head_dim,
+                     int32_t page_size, int32_t num_pages, int32_t max_blocks,
+                     int32_t causal, float softmax_scale,
+                     int32_t* status, void* stream);
+
+/*
+ * Batched page copy (generalises engine/kv_cache.py:189-207, the per-layer, per-page copy_
+ * loop of transfer_sequence; also copy-on-write of a shared partially filled page and
+ * live-page migration).  For every tensor i < n_tensors and pair p < n_pages:
+ *   dst_bases[i] + dst_ids[p] * dst_page_stride_bytes  <-  the first fill_slots[p] slots
+ *   (slot_bytes each) of  src_bases[i] + src_ids[p] * src_page_stride_bytes.
+ * src_bases/dst_bases are DEVICE arrays of n_tensors addresses (e.g. the K then V base of
+ * every layer); src_ids/dst_ids/fill_slots are DEVICE int32 arrays (fill_slots NULL = whole
+ * page of page_slots slots).  Ids outside [0, src_num_pages) / [0, dst_num_pages) are
+ * skipped and flagged in status.  Source and destination pages must not overlap.
+ * Bit-exact 16-byte copies; slot_bytes and page strides must be multiples of 16.
+ */
+int pkv_copy_pages(const uint64_t* src_bases, const uint64_t* dst_bases, int32_t n_tensors,
+                   const int32_t* src_ids, const int32_t* dst_ids, const int32_t* fill_slots,
+                   int32_t n_pages, int64_t src_page_stride_bytes, int64_t dst_page_stride_bytes,
+                   int64_t slot_bytes, int32_t page_slots,
+                   int32_t src_num_pages, int32_t dst_num_pages,
+                   int32_t* status, void* stream);
+
+/*
+ * Page gather / compaction into a fresh pool: pkv_copy_pages with dst_ids[p] = dst_first + p
+ * and whole pages.  Used to pack every live page of a pool into pages [0, n) of another.
+ */
+int pkv_gather_pages(const uint64_t* src_bases, const uint64_t* dst_bases, int32_t n_tensors,
+                     const int32_t* src_ids, int32_t n_pages, int32_t dst_first,
+                     int64_t src_page_stride_bytes, int64_t dst_page_stride_bytes,
+                     int64_t page_bytes, int32_t src_num_pages, int32_t dst_num_pages,
+                     int32_t* status, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PRISM_KV_H */

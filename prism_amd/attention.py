@@ -1,0 +1,294 @@
+"""flash_attn_with_kvcache drop-in over the gfx950 HIP kernels, plus the individual ops.
+
+Prism imports ``from flash_attn import flash_attn_with_kvcache`` (engine/executor.py:11,
+engine/speculative_executor.py:13) and calls it as
+``flash_attn_with_kvcache(q, k_cache, v_cache, k=k, v=v, cache_seqlens=sl, block_table=bt,
+causal=True)`` (engine/executor.py:119-120, :151-153, :260-261, :385-386;
+engine/speculative_executor.py:150-153).  This module provides a function of the same name and
+argument meaning:
+
+* ``q`` [B, s_q, n_heads, head_dim] bf16; ``k_cache``/``v_cache`` [num_pages, page_size, n_kv,
+  head_dim] bf16 (page stride free, inner dims contiguous) mutated in place by the append;
+* ``k``/``v`` [B, s_q, n_kv, head_dim] (optional) appended at ``cache_seqlens`` (int32 [B], the
+  length before the append) through ``block_table`` (int32 [B, max_blocks]);
+* query j attends keys ``t <= L_b - s_q + j`` when ``causal`` (bottom-right aligned), scale
+  ``softmax_scale`` (default 1/sqrt(head_dim)); query head h reads KV head h // (n_heads/n_kv);
+* returns a new bf16 ``out`` [B, s_q, n_heads, head_dim]; errors raise ``RuntimeError``.
+
+Calls are asynchronous on the caller's current stream, allocate only ``out`` (and a cached,
+grow-only split-K workspace per device), and can be captured in a HIP graph once the workspace
+has been sized by an eager call.
+"""
+from __future__ import annotations
+
+import math
+import threading
+
+import torch
+
+from . import _lib
+
+_BF16 = torch.bfloat16
+_ws_lock = threading.Lock()
+_workspaces: dict[int, torch.Tensor] = {}
+_status: dict[int, torch.Tensor] = {}
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_gpu(t: torch.Tensor, name: str) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name} must be a ROCm device tensor (got {t.device}); "
+                           "prism_amd has no CPU path")
+
+
+def status_tensor(device: torch.device) -> torch.Tensor:
+    """Per-device int32 the kernels OR error bits into (PKV_STATUS_BAD_PAGE = 1)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    t = _status.get(idx)
+    if t is None:
+        t = torch.zeros(1, dtype=torch.int32, device=device)
+        _status[idx] = t
+    return t
+
+
+def read_status(device: torch.device | str = "cuda", clear: bool = True) -> int:
+    """Synchronously read (and by default clear) the device status word."""
+    device = torch.device(device)
+    t = status_tensor(device)
+    v = int(t.item())
+    if clear:
+        t.zero_()
+    return v
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    with _ws_lock:
+        ws = _workspaces.get(idx)
+        if ws is None or ws.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    "split-K workspace must be sized by an eager call before HIP graph capture")
+            ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            _workspaces[idx] = ws
+        return ws
+
+
+def _rows(t: torch.Tensor, name: str, nheads: int, hd: int) -> tuple[int, int, int]:
+    if t.dtype != _BF16:
+        raise RuntimeError(f"{name} must be bfloat16, got {t.dtype}")
+    if t.dim() != 4 or t.shape[2] != nheads or t.shape[3] != hd:
+        raise RuntimeError(f"{name} has shape {tuple(t.shape)}, expected [B, s, {nheads}, {hd}]")
+    if t.stride(3) != 1:
+        raise RuntimeError(f"{name} must be contiguous in head_dim")
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor) -> tuple[int, int, int, int]:
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _require_gpu(t, name)
+        if t.dtype != _BF16:
+            raise RuntimeError(f"{name} must be bfloat16, got {t.dtype}")
+        if t.dim() != 4:
+            raise RuntimeError(f"{name} must be [num_pages, page_size, n_kv, head_dim]")
+    if k_cache.shape != v_cache.shape or k_cache.stride() != v_cache.stride():
+        raise RuntimeError("k_cache and v_cache must have the same shape and strides")
+    num_pages, page_size, n_kv, hd = k_cache.shape
+    if k_cache.stride()[1:] != (n_kv * hd, hd, 1):
+        raise RuntimeError("k_cache/v_cache must be contiguous within a page")
+    return num_pages, page_size, n_kv, hd
+
+
+def _check_table(block_table: torch.Tensor, cache_seqlens: torch.Tensor, batch: int, device) -> None:
+    if block_table.dtype != torch.int32 or cache_seqlens.dtype != torch.int32:
+        raise RuntimeError("block_table and cache_seqlens must be int32")
+    if block_table.dim() != 2 or block_table.shape[0] != batch or block_table.stride(1) != 1:
+        raise RuntimeError(f"block_table must be [B={batch}, max_blocks] with unit column stride")
+    if cache_seqlens.dim() != 1 or cache_seqlens.shape[0] != batch or cache_seqlens.stride(0) != 1:
+        raise RuntimeError(f"cache_seqlens must be a contiguous [B={batch}] tensor")
+    if block_table.device != device or cache_seqlens.device != device:
+        raise RuntimeError("block_table/cache_seqlens must live on the cache's device")
+
+
+def append_kv(k_cache, v_cache, k, v, cache_seqlens, block_table, *, status=None) -> None:
+    """Slot-mapped append only (the append half of flash_attn_with_kvcache)."""
+    num_pages, page_size, n_kv, hd = _check_cache(k_cache, v_cache)
+    batch, s_new = k.shape[0], k.shape[1]
+    ks = _rows(k, "k", n_kv, hd)
+    vs = _rows(v, "v", n_kv, hd)
+    if tuple(v.shape) != tuple(k.shape):
+        raise RuntimeError("k and v must have the same shape")
+    _check_table(block_table, cache_seqlens, batch, k_cache.device)
+    if batch == 0 or s_new == 0:
+        return
+    st = status if status is not None else status_tensor(k_cache.device)
+    lib = _lib.load()
+    rc = lib.pkv_append(
+        k.data_ptr(), *ks, v.data_ptr(), *vs,
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
+        block_table.data_ptr(), block_table.stride(0), cache_seqlens.data_ptr(),
+        batch, s_new, n_kv, hd, page_size, num_pages, block_table.shape[1],
+        st.data_ptr(), _stream_ptr(k_cache.device))
+    _lib.check(rc, "pkv_append")
+
+
+def flash_attn_with_kvcache(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    k: torch.Tensor | None = None,
+    v: torch.Tensor | None = None,
+    rotary_cos=None,
+    rotary_sin=None,
+    cache_seqlens: torch.Tensor | int | None = None,
+    cache_batch_idx=None,
+    cache_leftpad=None,
+    block_table: torch.Tensor | None = None,
+    softmax_scale: float | None = None,
+    causal: bool = False,
+    window_size=(-1, -1),
+    softcap: float = 0.0,
+    rotary_interleaved: bool = True,
+    alibi_slopes=None,
+    num_splits: int = 0,
+    return_softmax_lse: bool = False,
+    *,
+    out: torch.Tensor | None = None,
+    split_tokens: int = 0,
+    status: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Append k/v into the paged cache and attend (see module docstring for the contract).
+
+    Arguments Prism never passes (rotary_*, cache_batch_idx, cache_leftpad, window_size,
+    softcap, alibi_slopes, return_softmax_lse) must keep their defaults.  ``num_splits`` > 0
+    fixes the number of KV splits per sequence; ``split_tokens`` > 0 (a multiple of 32) fixes
+    the split length directly.
+    """
+    if rotary_cos is not None or rotary_sin is not None or cache_batch_idx is not None \
+            or cache_leftpad is not None or tuple(window_size) != (-1, -1) or softcap != 0.0 \
+            or alibi_slopes is not None or return_softmax_lse:
+        raise NotImplementedError("prism_amd.flash_attn_with_kvcache supports the arguments Prism uses: "
+                                  "q, k_cache, v_cache, k, v, cache_seqlens, block_table, "
+                                  "softmax_scale, causal, num_splits")
+    _require_gpu(q, "q")
+    num_pages, page_size, n_kv, hd = _check_cache(k_cache, v_cache)
+    if q.dim() != 4:
+        raise RuntimeError(f"q must be [B, s_q, n_heads, head_dim], got {tuple(q.shape)}")
+    batch, s_q, n_heads, qhd = q.shape
+    if qhd != hd:
+        raise RuntimeError(f"q head_dim {qhd} != cache head_dim {hd}")
+    if n_heads % n_kv:
+        raise RuntimeError(f"n_heads {n_heads} must be a multiple of n_kv {n_kv}")
+    qs = _rows(q, "q", n_heads, hd)
+    device = k_cache.device
+    if q.device != device:
+        raise RuntimeError("q must be on the cache's device")
+
+    if (k is None) != (v is None):
+        raise RuntimeError("k and v must both be given or both be None")
+    if k is not None:
+        if k.shape[0] != batch or k.shape[1] != s_q or tuple(v.shape) != tuple(k.shape):
+            raise RuntimeError("k/v must be [B, s_q, n_kv, head_dim] matching q")
+        ks = _rows(k, "k", n_kv, hd)
+        vs = _rows(v, "v", n_kv, hd)
+        kp, vp = k.data_ptr(), v.data_ptr()
+    else:
+        ks = vs = (0, 0, 0)
+        kp = vp = 0
+
+    if cache_seqlens is None:
+        raise RuntimeError("cache_seqlens is required")
+    if isinstance(cache_seqlens, int):
+        cache_seqlens = torch.full((batch,), cache_seqlens, dtype=torch.int32, device=device)
+    if block_table is None:
+        # a non-paged cache [B, seqlen, n_kv, hd] is one page per sequence
+        if num_pages != batch:
+            raise RuntimeError("without block_table, k_cache must be [B, seqlen_cache, n_kv, head_dim]")
+        block_table = torch.arange(batch, dtype=torch.int32, device=device).view(batch, 1)
+    _check_table(block_table, cache_seqlens, batch, device)
+    if page_size < 16 or page_size & (page_size - 1):
+        raise RuntimeError(f"page_size {page_size} must be a power of two >= 16")
+    max_blocks = block_table.shape[1]
+    scale = float(softmax_scale) if softmax_scale is not None else 1.0 / math.sqrt(hd)
+
+    if out is None:
+        out = torch.empty((batch, s_q, n_heads, hd), dtype=_BF16, device=device)
+    os_ = _rows(out, "out", n_heads, hd)
+    if batch == 0:
+        return out
+    st = status if status is not None else status_tensor(device)
+    lib = _lib.load()
+    stream = _stream_ptr(device)
+    g = n_heads // n_kv
+    if s_q * g <= 64:
+        if num_splits and num_splits > 0 and not split_tokens:
+            per_split = -(-(max_blocks * page_size) // num_splits)
+            split_tokens = max(32, -(-per_split // 32) * 32)
+        nbytes = lib.pkv_decode_workspace_bytes(batch, s_q, n_heads, n_kv, hd, page_size, max_blocks,
+                                                int(split_tokens))
+        ws = _workspace(device, nbytes)
+        rc = lib.pkv_decode_attn(
+            q.data_ptr(), *qs, kp, *ks, vp, *vs,
+            k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
+            block_table.data_ptr(), block_table.stride(0), cache_seqlens.data_ptr(),
+            out.data_ptr(), *os_,
+            ws.data_ptr() if ws is not None else 0, ws.numel() if ws is not None else 0,
+            batch, s_q, n_heads, n_kv, hd, page_size, num_pages, max_blocks,
+            1 if causal else 0, scale, int(split_tokens), st.data_ptr(), stream)
+        _lib.check(rc, "pkv_decode_attn")
+    else:
+        rc = lib.pkv_prefill_attn(
+            q.data_ptr(), *qs, kp, *ks, vp, *vs,
+            k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
+            block_table.data_ptr(), block_table.stride(0), cache_seqlens.data_ptr(),
+            out.data_ptr(), *os_,
+            batch, s_q, n_heads, n_kv, hd, page_size, num_pages, max_blocks,
+            1 if causal else 0, scale, st.data_ptr(), stream)
+        _lib.check(rc, "pkv_prefill_attn")
+    return out
+
+
+def decode_attention(q, k_cache, v_cache, k=None, v=None, *, cache_seqlens, block_table,
+                     causal=True, softmax_scale=None, split_tokens=0, out=None, status=None):
+    """Force the split-K decode kernel (s_q * n_heads / n_kv <= 64)."""
+    n_kv = k_cache.shape[2]
+    if q.shape[1] * (q.shape[2] // n_kv) > 64:
+        raise RuntimeError("decode_attention needs s_q * n_heads / n_kv <= 64")
+    return flash_attn_with_kvcache(q, k_cache, v_cache, k, v, cache_seqlens=cache_seqlens,
+                                   block_table=block_table, causal=causal, softmax_scale=softmax_scale,
+                                   split_tokens=split_tokens, out=out, status=status)
+
+
+def prefill_attention(q, k_cache, v_cache, k=None, v=None, *, cache_seqlens, block_table,
+                      causal=True, softmax_scale=None, out=None, status=None):
+    """Force the row-parallel prefill kernel (any s_q)."""
+    _require_gpu(q, "q")
+    num_pages, page_size, n_kv, hd = _check_cache(k_cache, v_cache)
+    batch, s_q, n_heads, _ = q.shape
+    qs = _rows(q, "q", n_heads, hd)
+    if k is not None:
+        ks, vs, kp, vp = _rows(k, "k", n_kv, hd), _rows(v, "v", n_kv, hd), k.data_ptr(), v.data_ptr()
+    else:
+        ks = vs = (0, 0, 0)
+        kp = vp = 0
+    _check_table(block_table, cache_seqlens, batch, k_cache.device)
+    if out is None:
+        out = torch.empty((batch, s_q, n_heads, hd), dtype=_BF16, device=q.device)
+    os_ = _rows(out, "out", n_heads, hd)
+    if batch == 0:
+        return out
+    st = status if status is not None else status_tensor(k_cache.device)
+    scale = float(softmax_scale) if softmax_scale is not None else 1.0 / math.sqrt(hd)
+    rc = _lib.load().pkv_prefill_attn(
+        q.data_ptr(), *qs, kp, *ks, vp, *vs,
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
+        block_table.data_ptr(), block_table.stride(0), cache_seqlens.data_ptr(),
+        out.data_ptr(), *os_, batch, s_q, n_heads, n_kv, hd, page_size, num_pages,
+        block_table.shape[1], 1 if causal else 0, scale, st.data_ptr(), _stream_ptr(q.device))
+    _lib.check(rc, "pkv_prefill_attn")
+    return out

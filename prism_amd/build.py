@@ -1,0 +1,80 @@
+"""Build libprism_kv.so (the gfx950 HIP kernels behind include/prism_kv.h) in-tree.
+
+Usage: python -m prism_amd.build   (or prism_amd.build.build() from Python).
+
+Every .hip file under prism_amd/csrc is compiled by hipcc for gfx950 into one object each (in
+parallel), then linked into prism_amd/libprism_kv.so.  The .so is what the ctypes loader
+(prism_amd/_lib.py) opens; it is git-ignored but travels with the source tree to a GPU host.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR / "csrc"
+LIB_NAME = "libprism_kv.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+BUILD_DIR = PKG_DIR / "_build"
+ARCH = "gfx950"
+
+# -packed-fp32-ops off: hipcc must not emit packed FP32 arithmetic (v_pk_fma_f32 and friends)
+# from ordinary float code; the host pass prints a harmless "not a recognized feature" warning.
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: cannot build libprism_kv.so")
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(
+        line for line in proc.stdout.splitlines() if "is not a recognized feature for this target" not in line
+    )
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip():
+        print(out, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every csrc/*.hip for gfx950 and link libprism_kv.so.  Always rebuilds."""
+    hipcc = _hipcc()
+    BUILD_DIR.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    objs = [BUILD_DIR / (s.stem + ".o") for s in sources]
+    cmds = [[hipcc, *HIPCC_FLAGS, "-c", str(s), "-o", str(o)] for s, o in zip(sources, objs)]
+    workers = min(len(cmds), max(1, (os.cpu_count() or 2) // 2), 8)
+    with cf.ThreadPoolExecutor(workers) as ex:
+        for cmd, fut in zip(cmds, [ex.submit(_run, c) for c in cmds]):
+            if verbose:
+                print(" ".join(cmd))
+            fut.result()
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH}")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build(verbose=True)

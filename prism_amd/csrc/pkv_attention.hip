@@ -1,0 +1,725 @@
+// Paged attention for gfx950 (MI355X): decode / speculative verify (split-K over the KV range)
+// and varlen chunked prefill (query rows spread over waves), both over Prism's paged cache.
+//
+// Replaces flash_attn_with_kvcache as Prism calls it (engine/executor.py:119-120, :151-153,
+// :260-261, :385-386; engine/speculative_executor.py:150-153): new K/V rows are appended at
+// cache_seqlens[b], and query j of sequence b (L_b keys after the append) attends to keys
+// t <= L_b - s_q + j (causal, bottom-right aligned) through the block table; query head hq
+// reads KV head hq / g with g = n_heads / n_kv.
+//
+// Orientation.  All query rows that read one KV head (row = j * g + head-in-group) are the N
+// side of v_mfma_f32_16x16x32_bf16, 16 rows per N tile; 32-token KV tiles are the M side:
+//
+//   S^T[tok, row] = K[tok, :] . Q[row, :]          A = K rows straight from memory (16 B/lane),
+//                                                  B = Q^T held in registers for the whole call
+//   O^T[d, row]  += V^T[d, tok] . P^T[tok, row]     A = V^T repacked in registers,
+//                                                  B = P^T = the S^T accumulator, in place
+//
+// The S^T accumulator a lane holds (4 tokens x 1 row per MFMA) is exactly the P^T operand the
+// PV MFMA wants, and all softmax statistics of a lane's row live in that lane, so the
+// online-softmax rescale of O needs no cross-lane traffic; only the tile max is reduced across
+// the four 16-lane groups.  V rows arrive head_dim-contiguous: each lane loads 8 tokens x
+// head_dim/16 elements and transposes them with byte permutes into the token-major V^T operand.
+// Every K/V byte of a (sequence, KV head) is fetched once per query-row tile.
+#include <math.h>
+
+#include "pkv_common.h"
+
+namespace pkv {
+
+struct AttnParams {
+  const uint16_t* q;
+  int64_t q_sb, q_ss, q_sh;
+  const uint16_t* k_new;
+  int64_t kn_sb, kn_ss, kn_sh;
+  const uint16_t* v_new;
+  int64_t vn_sb, vn_ss, vn_sh;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int64_t page_stride;
+  const int32_t* block_table;
+  int64_t bt_stride;
+  const int32_t* seqlens;
+  uint16_t* out;
+  int64_t o_sb, o_ss, o_sh;
+  float* ws_o;   // [batch, n_kv, max_splits, R, head_dim] unnormalised split partials
+  float* ws_ml;  // [batch, n_kv, max_splits, R, 2] (row max in log2 units, row sum of exp2)
+  int32_t* status;
+  int s_q, g, R, n_kv, log2_page, num_pages, max_blocks, split_tokens, max_splits;
+  int causal, has_new;
+  float scale_log2;  // softmax_scale * log2(e)
+};
+
+__device__ __forceinline__ float max_over_quads(float v) {
+  // max over the four lanes {l, l^16, l^32, l^48} that hold the same query row.
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+
+__device__ __forceinline__ float sum_over_quads(float v) {
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// One lane's slice of a V row: head_dim/16 bf16 values as 32-bit words.
+template <int HD>
+struct VRow {
+  uint32_t w[HD / 32];
+};
+
+template <int HD>
+__device__ __forceinline__ void load_vrow(VRow<HD>& r, const uint16_t* ptr) {
+  if constexpr (HD == 128) {
+    const u32x4 v = ld16(ptr);
+    r.w[0] = v[0]; r.w[1] = v[1]; r.w[2] = v[2]; r.w[3] = v[3];
+  } else {
+    const u32x2 v = ld8(ptr);
+    r.w[0] = v[0]; r.w[1] = v[1];
+  }
+}
+
+// Keys of sequence b: (cache length c, total L).  A length outside what the block table can
+// address is flagged and clamped, so work and workspace indices stay bounded.
+__device__ __forceinline__ void seq_lengths(const AttnParams& p, int b, int& c, int& L) {
+  const int cap = p.max_blocks << p.log2_page;
+  c = p.seqlens[b];
+  L = c + (p.has_new ? p.s_q : 0);
+  if (c < 0 || L > cap) {
+    if (threadIdx.x == 0) flag_status(p.status, PKV_STATUS_BAD_PAGE);
+    c = min(max(c, 0), cap);
+    L = min(c + (p.has_new ? p.s_q : 0), cap);
+  }
+}
+
+__device__ __forceinline__ int num_splits(const AttnParams& p, int L) {
+  const int n = L > 0 ? (L + p.split_tokens - 1) / p.split_tokens : 1;
+  return min(n, p.max_splits);
+}
+
+// Per-(sequence, KV head) view used by the wave routine.
+struct SeqView {
+  int b, h, c, t_end;
+  const int32_t* bt;
+};
+
+// Address of the head-h row of token t, or nullptr when t is out of range or its page id is
+// bad.  Rows being appended by this call (t >= c) come straight from k_new / v_new, so no
+// workgroup ever reads a cache slot that the same call writes.
+__device__ __forceinline__ const uint16_t* kv_row(const AttnParams& p, const SeqView& sv, bool is_v, int t,
+                                                  int pid, int hd) {
+  if (t >= sv.t_end) return nullptr;
+  if (p.has_new && t >= sv.c) {
+    const int j = t - sv.c;
+    return is_v ? p.v_new + sv.b * p.vn_sb + j * p.vn_ss + sv.h * p.vn_sh
+                : p.k_new + sv.b * p.kn_sb + j * p.kn_ss + sv.h * p.kn_sh;
+  }
+  if (pid < 0 || pid >= p.num_pages) {
+    flag_status(p.status, PKV_STATUS_BAD_PAGE);
+    return nullptr;
+  }
+  return (is_v ? p.v_cache : p.k_cache) + int64_t(pid) * p.page_stride +
+         int64_t(t & ((1 << p.log2_page) - 1)) * (p.n_kv * hd) + sv.h * hd;
+}
+
+// Load the Q^T operand for the 16*NT rows starting at row0 and the last key each row may see.
+template <int HD, int NT>
+__device__ __forceinline__ void load_q(const AttnParams& p, const SeqView& sv, int L, int row0,
+                                       bf16x8 (&qf)[NT][HD / 32], int (&lim)[NT]) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15;
+  const int lq = lane >> 4;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int rr = row0 + li + 16 * nt;
+    if (rr < p.R) {
+      const int j = rr / p.g;
+      const int hq = rr - j * p.g;
+      const uint16_t* base = p.q + sv.b * p.q_sb + j * p.q_ss + (sv.h * p.g + hq) * p.q_sh + 8 * lq;
+#pragma unroll
+      for (int kk = 0; kk < HD / 32; ++kk) qf[nt][kk] = __builtin_bit_cast(bf16x8, ld16(base + 32 * kk));
+      const int last = p.causal ? (L - p.s_q + j) : (L - 1);
+      lim[nt] = min(last, sv.t_end - 1);
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < HD / 32; ++kk) qf[nt][kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+      lim[nt] = -1;
+    }
+  }
+}
+
+// Online-softmax attention of one wave's 16*NT query rows over the 32-token tiles starting at
+// token T_first, T_step apart, below T_stop.  Accumulates into (m_run, l_run, acc); l_run is a
+// per-lane partial (sum over the lane's own tokens) to be reduced with sum_over_quads.
+// SPLIT_P feeds P to the PV MFMA as a bf16 hi + lo pair (two MFMAs) instead of one bf16
+// rounding: decode has an order of magnitude of MFMA headroom, and short contexts then keep the
+// output error down to the output's own bf16 rounding.
+template <int HD, int NT, bool SPLIT_P>
+__device__ __forceinline__ void wave_attend(const AttnParams& p, const SeqView& sv, const bf16x8 (&qf)[NT][HD / 32],
+                                            const int (&lim)[NT], int T_first, int T_stop, int T_step,
+                                            float (&m_run)[NT], float (&l_run)[NT], f32x4 (&acc)[NT][HD / 16]) {
+  constexpr int KK = HD / 32;
+  constexpr int DPL = HD / 16;
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15;
+  const int lq = lane >> 4;
+
+  for (int T0 = T_first; T0 < T_stop; T0 += T_step) {
+    // Page of each 16-token half (the same page whenever page_size >= 32).
+    const int colA = T0 >> p.log2_page;
+    const int colB = (T0 + 16) >> p.log2_page;
+    const int pidA = colA < p.max_blocks ? sv.bt[colA] : -1;
+    const int pidB = colB < p.max_blocks ? sv.bt[colB] : -1;
+
+    // K: lane (li, lq) supplies M-row li of QK tile a = token T0 + 8*(li/4) + 4a + li%4 and
+    // head-row elements [32kk + 8lq, +8).
+    u32x4 kr[2][KK];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const int tt = 8 * (li >> 2) + 4 * a + (li & 3);
+      const uint16_t* kp = kv_row(p, sv, false, T0 + tt, tt < 16 ? pidA : pidB, HD);
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) kr[a][kk] = kp ? ld16(kp + 32 * kk + 8 * lq) : u32x4{0u, 0u, 0u, 0u};
+    }
+    // V: lane (li, lq) loads tokens T0 + 8lq + e (e < 8), head-row elements [DPL*li, +DPL).
+    VRow<HD> vr[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int tt = 8 * lq + e;
+      const uint16_t* vp = kv_row(p, sv, true, T0 + tt, tt < 16 ? pidA : pidB, HD);
+      if (vp) {
+        load_vrow<HD>(vr[e], vp + DPL * li);
+      } else {
+#pragma unroll
+        for (int w = 0; w < HD / 32; ++w) vr[e].w[w] = 0u;
+      }
+    }
+
+    // V^T operands: PV MFMA n covers head-dim elements d = DPL*i + n (i = M row = lane li);
+    // element e of the operand is token T0 + 8lq + e.
+    bf16x8 vt[DPL];
+#pragma unroll
+    for (int n = 0; n < DPL; ++n) {
+      const int w = n >> 1;
+      u32x4 pk;
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        const uint32_t x0 = vr[2 * pp].w[w];
+        const uint32_t x1 = vr[2 * pp + 1].w[w];
+        pk[pp] = (n & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
+      }
+      vt[n] = __builtin_bit_cast(bf16x8, pk);
+    }
+
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      f32x4 s[2];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        s[a] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+          s[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[a][kk]), qf[nt][kk], s[a],
+                                                        0, 0, 0);
+      }
+      // s[a][r]: score of token T0 + 8lq + 4a + r against query row li + 16nt.
+      float x[8];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = T0 + 8 * lq + 4 * a + r;
+          const float v = (t <= lim[nt]) ? s[a][r] * p.scale_log2 : -INFINITY;
+          x[4 * a + r] = v;
+          mx = fmaxf(mx, v);
+        }
+      }
+      mx = max_over_quads(mx);
+      const float m_new = fmaxf(m_run[nt], mx);
+      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = fast_exp2(m_run[nt] - m_use);
+      float psum = 0.f;
+      u32x4 pk, pk_lo;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float p0 = fast_exp2(x[e] - m_use);
+        const float p1 = fast_exp2(x[e + 1] - m_use);
+        psum += p0 + p1;
+        pk[e >> 1] = pack_bf16x2(p0, p1);
+        if constexpr (SPLIT_P) {
+          // P = hi + lo with both halves bf16: the PV product then carries ~16 mantissa bits of P
+          const float h0 = bf16_bits_to_f32(pk[e >> 1] & 0xffffu);
+          const float h1 = bf16_bits_to_f32(pk[e >> 1] >> 16);
+          pk_lo[e >> 1] = pack_bf16x2(p0 - h0, p1 - h1);
+        }
+      }
+      l_run[nt] = l_run[nt] * alpha + psum;
+      m_run[nt] = m_new;
+      const bf16x8 pb = __builtin_bit_cast(bf16x8, pk);
+#pragma unroll
+      for (int n = 0; n < DPL; ++n) {
+        acc[nt][n] *= alpha;
+        acc[nt][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[n], pb, acc[nt][n], 0, 0, 0);
+        if constexpr (SPLIT_P)
+          acc[nt][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[n], __builtin_bit_cast(bf16x8, pk_lo),
+                                                              acc[nt][n], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// Copy the rows of this call that land in tokens [a0, a1) of (b, h) into the cache.
+template <int HD>
+__device__ __forceinline__ void append_rows(const AttnParams& p, const SeqView& sv, int a0, int a1, int tid,
+                                            int nthreads) {
+  constexpr int CPR = HD / 8;
+  const int n_items = (a1 - a0) * 2 * CPR;
+  for (int idx = tid; idx < n_items; idx += nthreads) {
+    const int row = idx / (2 * CPR);
+    const int rem = idx - row * (2 * CPR);
+    const bool is_v = rem >= CPR;
+    const int c8 = is_v ? rem - CPR : rem;
+    const int t = a0 + row;
+    const int j = t - sv.c;
+    const int col = t >> p.log2_page;
+    const int pid = col < p.max_blocks ? sv.bt[col] : -1;
+    if (pid < 0 || pid >= p.num_pages) {
+      flag_status(p.status, PKV_STATUS_BAD_PAGE);
+      continue;
+    }
+    const int64_t dst =
+        int64_t(pid) * p.page_stride + int64_t(t & ((1 << p.log2_page) - 1)) * (p.n_kv * HD) + sv.h * HD + c8 * 8;
+    const uint16_t* src = is_v ? p.v_new + sv.b * p.vn_sb + j * p.vn_ss + sv.h * p.vn_sh
+                               : p.k_new + sv.b * p.kn_sb + j * p.kn_ss + sv.h * p.kn_sh;
+    st16((is_v ? p.v_cache : p.k_cache) + dst, ld16(src + c8 * 8));
+  }
+}
+
+__device__ __forceinline__ void store_out_row8(const AttnParams& p, int b, int h, int row, int d0, const float (&o)[8],
+                                               float lsum) {
+  const int j = row / p.g;
+  const int hq = row - j * p.g;
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  u32x4 ov;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(o[2 * k] * inv, o[2 * k + 1] * inv);
+  st16(p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + d0, ov);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Decode / verify: grid (split, KV head, sequence).  The W waves take interleaved 32-token tiles
+// of the split and merge (m, l, O) through LDS.  A sequence whose keys fit one split writes the
+// bf16 output directly; otherwise the split writes its partial for combine_kernel.
+// ---------------------------------------------------------------------------------------------
+template <int HD, int NT, int W>
+__global__ __launch_bounds__(64 * W) void decode_kernel(const AttnParams p) {
+  constexpr int DPL = HD / 16;
+  constexpr int ROWS = 16 * NT;
+  constexpr int CPR = HD / 8;
+
+  __shared__ float sm_o[W][ROWS][HD + 4];
+  __shared__ float sm_m[W][ROWS];
+  __shared__ float sm_l[W][ROWS];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15;
+  const int lq = lane >> 4;
+  const int split = blockIdx.x;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+
+  int c, L;
+  seq_lengths(p, b, c, L);
+  const int t_begin = split * p.split_tokens;
+  if (split > 0 && t_begin >= L) return;
+  const int n_split_b = num_splits(p, L);
+  SeqView sv;
+  sv.b = b;
+  sv.h = h;
+  sv.c = c;
+  sv.t_end = min(t_begin + p.split_tokens, L);
+  sv.bt = p.block_table + int64_t(b) * p.bt_stride;
+
+  if (p.has_new) append_rows<HD>(p, sv, max(max(c, t_begin), 0), sv.t_end, threadIdx.x, 64 * W);
+
+  bf16x8 qf[NT][HD / 32];
+  int lim[NT];
+  load_q<HD, NT>(p, sv, L, 0, qf, lim);
+
+  float m_run[NT], l_run[NT];
+  f32x4 acc[NT][DPL];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    m_run[nt] = -INFINITY;
+    l_run[nt] = 0.f;
+#pragma unroll
+    for (int n = 0; n < DPL; ++n) acc[nt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  // The last query row (j = s_q - 1) sees every key of the split, so the whole split is walked.
+  wave_attend<HD, NT, true>(p, sv, qf, lim, t_begin + 32 * wave, sv.t_end, 32 * W, m_run, l_run, acc);
+
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int row = li + 16 * nt;
+    const float l_tot = sum_over_quads(l_run[nt]);
+    if (lq == 0) {
+      sm_m[wave][row] = m_run[nt];
+      sm_l[wave][row] = l_tot;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int n = 0; n < DPL; ++n) sm_o[wave][row][DPL * (4 * lq + r) + n] = acc[nt][n][r];
+  }
+  __syncthreads();
+
+  const int n_items = p.R * CPR;
+  for (int idx = threadIdx.x; idx < n_items; idx += 64 * W) {
+    const int row = idx / CPR;
+    const int d0 = (idx - row * CPR) * 8;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) M = fmaxf(M, sm_m[w][row]);
+    const float M_use = (M == -INFINITY) ? 0.f : M;
+    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float lsum = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float f = fast_exp2(sm_m[w][row] - M_use);
+      lsum += f * sm_l[w][row];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) o[k] += f * sm_o[w][row][d0 + k];
+    }
+    if (n_split_b == 1) {
+      store_out_row8(p, b, h, row, d0, o, lsum);
+    } else {
+      const int64_t slot = (int64_t(b * p.n_kv + h) * p.max_splits + split) * p.R + row;
+      float* dst = p.ws_o + slot * HD + d0;
+      *reinterpret_cast<f32x4*>(dst) = f32x4{o[0], o[1], o[2], o[3]};
+      *reinterpret_cast<f32x4*>(dst + 4) = f32x4{o[4], o[5], o[6], o[7]};
+      if (d0 == 0) {
+        p.ws_ml[slot * 2] = M;
+        p.ws_ml[slot * 2 + 1] = lsum;
+      }
+    }
+  }
+}
+
+// Log-sum-exp combine of the split partials of every (sequence, KV head) with > 1 split.
+template <int HD>
+__global__ __launch_bounds__(256) void combine_kernel(const AttnParams p) {
+  constexpr int CPR = HD / 8;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  int c, L;
+  seq_lengths(p, b, c, L);
+  const int n_split_b = num_splits(p, L);
+  if (n_split_b <= 1) return;
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= p.R * CPR) return;
+  const int row = idx / CPR;
+  const int d0 = (idx - row * CPR) * 8;
+  const int64_t base = int64_t(b * p.n_kv + h) * p.max_splits * p.R + row;
+  float M = -INFINITY;
+  for (int s = 0; s < n_split_b; ++s) M = fmaxf(M, p.ws_ml[(base + int64_t(s) * p.R) * 2]);
+  const float M_use = (M == -INFINITY) ? 0.f : M;
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float lsum = 0.f;
+  for (int s = 0; s < n_split_b; ++s) {
+    const int64_t slot = base + int64_t(s) * p.R;
+    const float f = fast_exp2(p.ws_ml[slot * 2] - M_use);
+    lsum += f * p.ws_ml[slot * 2 + 1];
+    const f32x4 x0 = *reinterpret_cast<const f32x4*>(p.ws_o + slot * HD + d0);
+    const f32x4 x1 = *reinterpret_cast<const f32x4*>(p.ws_o + slot * HD + d0 + 4);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      o[k] += f * x0[k];
+      o[4 + k] += f * x1[k];
+    }
+  }
+  store_out_row8(p, b, h, row, d0, o, lsum);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Prefill: grid (row tile, KV head, sequence).  Each wave owns 16*NT consecutive query rows and
+// walks every KV tile its rows can see (causal: up to the wave's last visible key); the W waves
+// of a workgroup read the same tiles at about the same time, so the second and later reads hit
+// the CU's L1.  No split-K: each wave normalises and writes its own rows.  Row tile 0 appends
+// the new rows of (b, h) to the cache; reads of those rows go to k_new / v_new.
+// ---------------------------------------------------------------------------------------------
+template <int HD, int NT, int W>
+__global__ __launch_bounds__(64 * W) void prefill_kernel(const AttnParams p) {
+  constexpr int DPL = HD / 16;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15;
+  const int lq = lane >> 4;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+
+  int c, L;
+  seq_lengths(p, b, c, L);
+  SeqView sv;
+  sv.b = b;
+  sv.h = h;
+  sv.c = c;
+  sv.t_end = L;
+  sv.bt = p.block_table + int64_t(b) * p.bt_stride;
+
+  if (p.has_new && blockIdx.x == 0) append_rows<HD>(p, sv, max(c, 0), L, threadIdx.x, 64 * W);
+
+  const int row0 = (blockIdx.x * W + wave) * 16 * NT;
+  if (row0 >= p.R) return;
+
+  bf16x8 qf[NT][HD / 32];
+  int lim[NT];
+  load_q<HD, NT>(p, sv, L, row0, qf, lim);
+  // rows increase with j, so the wave's last row bounds every row's visible range
+  const int last_row = min(row0 + 16 * NT, p.R) - 1;
+  const int t_stop = p.causal ? min(L, L - p.s_q + last_row / p.g + 1) : L;
+
+  float m_run[NT], l_run[NT];
+  f32x4 acc[NT][DPL];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    m_run[nt] = -INFINITY;
+    l_run[nt] = 0.f;
+#pragma unroll
+    for (int n = 0; n < DPL; ++n) acc[nt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  wave_attend<HD, NT, false>(p, sv, qf, lim, 0, t_stop, 32, m_run, l_run, acc);
+
+  // acc[nt][n][r] = O[row li + 16nt][d = DPL*(4lq + r) + n]: the lane owns 4*DPL consecutive
+  // head-dim elements of its row, starting at 4*DPL*lq.
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int row = row0 + li + 16 * nt;
+    const float lsum = sum_over_quads(l_run[nt]);
+    if (row >= p.R) continue;
+    const int j = row / p.g;
+    const int hq = row - j * p.g;
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    uint16_t* dst = p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + 4 * DPL * lq;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if constexpr (DPL == 8) {
+        u32x4 ov;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[nt][2 * k][r] * inv, acc[nt][2 * k + 1][r] * inv);
+        st16(dst + DPL * r, ov);
+      } else {
+        u32x2 ov;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) ov[k] = pack_bf16x2(acc[nt][2 * k][r] * inv, acc[nt][2 * k + 1][r] * inv);
+        *reinterpret_cast<u32x2*>(dst + DPL * r) = ov;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------------------------
+static int choose_split_tokens(int split_tokens) { return split_tokens > 0 ? split_tokens : 512; }
+
+static int64_t max_splits_for(int split_tokens, int page_size, int max_blocks) {
+  const int64_t cap = int64_t(max_blocks) * page_size;
+  const int64_t n = (cap + split_tokens - 1) / split_tokens;
+  return n > 0 ? n : 1;
+}
+
+static size_t ws_floats_o(int batch, int R, int n_kv, int head_dim, int64_t max_splits) {
+  return size_t(batch) * n_kv * size_t(max_splits) * R * head_dim;
+}
+
+static size_t ws_bytes(int batch, int R, int n_kv, int head_dim, int64_t max_splits) {
+  const size_t rows = size_t(batch) * n_kv * size_t(max_splits) * R;
+  return (ws_floats_o(batch, R, n_kv, head_dim, max_splits) + rows * 2) * sizeof(float);
+}
+
+static int validate_attn(const char* fn, const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, const void* k_new,
+                         int64_t kn_sb, int64_t kn_ss, int64_t kn_sh, const void* v_new, int64_t vn_sb, int64_t vn_ss,
+                         int64_t vn_sh, void* k_cache, void* v_cache, int64_t page_stride, const int32_t* block_table,
+                         int64_t bt_stride, const int32_t* seqlens, const void* out, int64_t o_sb, int64_t o_ss,
+                         int64_t o_sh, int batch, int s_q, int n_heads, int n_kv, int head_dim, int page_size,
+                         int num_pages, int max_blocks, float softmax_scale) {
+  int rc = validate_paged(fn, k_cache, v_cache, page_stride, block_table, bt_stride, seqlens, batch, n_kv, head_dim,
+                          page_size, num_pages, max_blocks);
+  if (rc) return rc;
+  if (!q || !out) return fail(PKV_EINVAL, "%s: null q/out", fn);
+  if (s_q <= 0) return fail(PKV_EINVAL, "%s: s_q %d must be >= 1", fn, s_q);
+  if (n_heads <= 0 || n_heads % n_kv)
+    return fail(PKV_EINVAL, "%s: n_heads %d not a multiple of n_kv %d", fn, n_heads, n_kv);
+  if ((k_new == nullptr) != (v_new == nullptr))
+    return fail(PKV_EINVAL, "%s: k_new and v_new must both be given or both be null", fn);
+  if ((rc = validate_rows(fn, "q", q, q_sb, q_ss, q_sh))) return rc;
+  if ((rc = validate_rows(fn, "out", out, o_sb, o_ss, o_sh))) return rc;
+  if (k_new) {
+    if ((rc = validate_rows(fn, "k_new", k_new, kn_sb, kn_ss, kn_sh))) return rc;
+    if ((rc = validate_rows(fn, "v_new", v_new, vn_sb, vn_ss, vn_sh))) return rc;
+  }
+  if (!(softmax_scale > 0.f) || !isfinite(softmax_scale)) return fail(PKV_EINVAL, "%s: bad softmax_scale", fn);
+  if (batch > 65535 || n_kv > 65535) return fail(PKV_EINVAL, "%s: batch/n_kv exceed the grid limit", fn);
+  return PKV_OK;
+}
+
+static void fill_params(AttnParams& p, const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, const void* k_new,
+                        int64_t kn_sb, int64_t kn_ss, int64_t kn_sh, const void* v_new, int64_t vn_sb, int64_t vn_ss,
+                        int64_t vn_sh, void* k_cache, void* v_cache, int64_t page_stride, const int32_t* block_table,
+                        int64_t bt_stride, const int32_t* seqlens, void* out, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+                        int s_q, int n_heads, int n_kv, int page_size, int num_pages, int max_blocks, int causal,
+                        float softmax_scale, int32_t* status) {
+  p.q = static_cast<const uint16_t*>(q);
+  p.q_sb = q_sb; p.q_ss = q_ss; p.q_sh = q_sh;
+  p.k_new = static_cast<const uint16_t*>(k_new);
+  p.kn_sb = kn_sb; p.kn_ss = kn_ss; p.kn_sh = kn_sh;
+  p.v_new = static_cast<const uint16_t*>(v_new);
+  p.vn_sb = vn_sb; p.vn_ss = vn_ss; p.vn_sh = vn_sh;
+  p.k_cache = static_cast<uint16_t*>(k_cache);
+  p.v_cache = static_cast<uint16_t*>(v_cache);
+  p.page_stride = page_stride;
+  p.block_table = block_table;
+  p.bt_stride = bt_stride;
+  p.seqlens = seqlens;
+  p.out = static_cast<uint16_t*>(out);
+  p.o_sb = o_sb; p.o_ss = o_ss; p.o_sh = o_sh;
+  p.ws_o = nullptr;
+  p.ws_ml = nullptr;
+  p.status = status;
+  p.s_q = s_q;
+  p.g = n_heads / n_kv;
+  p.R = s_q * p.g;
+  p.n_kv = n_kv;
+  p.log2_page = ilog2(page_size);
+  p.num_pages = num_pages;
+  p.max_blocks = max_blocks;
+  p.split_tokens = 1 << 30;
+  p.max_splits = 1;
+  p.causal = causal ? 1 : 0;
+  p.has_new = k_new ? 1 : 0;
+  p.scale_log2 = softmax_scale * 1.4426950408889634f;
+}
+
+template <int HD, int NT, int W>
+static void launch_decode_t(const AttnParams& p, int batch, hipStream_t stream) {
+  dim3 grid(p.max_splits, p.n_kv, batch);
+  decode_kernel<HD, NT, W><<<grid, 64 * W, 0, stream>>>(p);
+  if (p.max_splits > 1) {
+    dim3 cgrid((p.R * (HD / 8) + 255) / 256, p.n_kv, batch);
+    combine_kernel<HD><<<cgrid, 256, 0, stream>>>(p);
+  }
+}
+
+template <int HD>
+static void launch_decode_hd(const AttnParams& p, int batch, hipStream_t stream) {
+  switch ((p.R + 15) / 16) {
+    case 1: launch_decode_t<HD, 1, 4>(p, batch, stream); break;
+    case 2: launch_decode_t<HD, 2, 4>(p, batch, stream); break;
+    case 3: launch_decode_t<HD, 3, 2>(p, batch, stream); break;
+    default: launch_decode_t<HD, 4, 2>(p, batch, stream); break;
+  }
+}
+
+constexpr int kPrefillNT = 2;
+constexpr int kPrefillW = 4;
+
+template <int HD>
+static void launch_prefill_hd(const AttnParams& p, int batch, hipStream_t stream) {
+  constexpr int rows_per_wg = 16 * kPrefillNT * kPrefillW;
+  dim3 grid((p.R + rows_per_wg - 1) / rows_per_wg, p.n_kv, batch);
+  prefill_kernel<HD, kPrefillNT, kPrefillW><<<grid, 64 * kPrefillW, 0, stream>>>(p);
+}
+
+}  // namespace pkv
+
+extern "C" size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv,
+                                             int32_t head_dim, int32_t page_size, int32_t max_blocks,
+                                             int32_t split_tokens) {
+  using namespace pkv;
+  if (batch <= 0 || s_q <= 0 || n_kv <= 0 || n_heads <= 0 || max_blocks <= 0 || page_size <= 0 || head_dim <= 0)
+    return 0;
+  const int st = choose_split_tokens(split_tokens);
+  const int64_t ms = max_splits_for(st, page_size, max_blocks);
+  if (ms <= 1) return 0;
+  return ws_bytes(batch, s_q * (n_heads / n_kv), n_kv, head_dim, ms);
+}
+
+extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, const void* k_new,
+                               int64_t kn_sb, int64_t kn_ss, int64_t kn_sh, const void* v_new, int64_t vn_sb,
+                               int64_t vn_ss, int64_t vn_sh, void* k_cache, void* v_cache, int64_t cache_page_stride,
+                               const int32_t* block_table, int64_t bt_stride, const int32_t* cache_seqlens, void* out,
+                               int64_t o_sb, int64_t o_ss, int64_t o_sh, void* workspace, size_t workspace_bytes,
+                               int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv, int32_t head_dim,
+                               int32_t page_size, int32_t num_pages, int32_t max_blocks, int32_t causal,
+                               float softmax_scale, int32_t split_tokens, int32_t* status, void* stream) {
+  using namespace pkv;
+  clear_error();
+  const char* fn = "pkv_decode_attn";
+  int rc = validate_attn(fn, q, q_sb, q_ss, q_sh, k_new, kn_sb, kn_ss, kn_sh, v_new, vn_sb, vn_ss, vn_sh, k_cache,
+                         v_cache, cache_page_stride, block_table, bt_stride, cache_seqlens, out, o_sb, o_ss, o_sh,
+                         batch, s_q, n_heads, n_kv, head_dim, page_size, num_pages, max_blocks, softmax_scale);
+  if (rc) return rc;
+  const int R = s_q * (n_heads / n_kv);
+  if (R > 64) return fail(PKV_EINVAL, "%s: s_q * n_heads / n_kv = %d > 64; use pkv_prefill_attn", fn, R);
+  const int st = choose_split_tokens(split_tokens);
+  if (st % 32) return fail(PKV_EINVAL, "%s: split_tokens %d must be a positive multiple of 32", fn, st);
+  const int64_t ms = max_splits_for(st, page_size, max_blocks);
+  if (ms > 65535) return fail(PKV_EINVAL, "%s: %lld splits exceed the grid limit", fn, (long long)ms);
+  if (batch == 0) return PKV_OK;
+
+  AttnParams p;
+  fill_params(p, q, q_sb, q_ss, q_sh, k_new, kn_sb, kn_ss, kn_sh, v_new, vn_sb, vn_ss, vn_sh, k_cache, v_cache,
+              cache_page_stride, block_table, bt_stride, cache_seqlens, out, o_sb, o_ss, o_sh, s_q, n_heads, n_kv,
+              page_size, num_pages, max_blocks, causal, softmax_scale, status);
+  p.split_tokens = st;
+  p.max_splits = int(ms);
+  if (ms > 1) {
+    const size_t need = ws_bytes(batch, R, n_kv, head_dim, ms);
+    if (!workspace || workspace_bytes < need)
+      return fail(PKV_ENOSPC, "%s: workspace %zu bytes < %zu needed", fn, workspace_bytes, need);
+    if (!aligned16(workspace)) return fail(PKV_EINVAL, "%s: workspace not 16-byte aligned", fn);
+    p.ws_o = static_cast<float*>(workspace);
+    p.ws_ml = p.ws_o + ws_floats_o(batch, R, n_kv, head_dim, ms);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (head_dim == 128)
+    launch_decode_hd<128>(p, batch, s);
+  else
+    launch_decode_hd<64>(p, batch, s);
+  return check_launch(fn);
+}
+
+extern "C" int pkv_prefill_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, const void* k_new,
+                                int64_t kn_sb, int64_t kn_ss, int64_t kn_sh, const void* v_new, int64_t vn_sb,
+                                int64_t vn_ss, int64_t vn_sh, void* k_cache, void* v_cache, int64_t cache_page_stride,
+                                const int32_t* block_table, int64_t bt_stride, const int32_t* cache_seqlens, void* out,
+                                int64_t o_sb, int64_t o_ss, int64_t o_sh, int32_t batch, int32_t s_q, int32_t n_heads,
+                                int32_t n_kv, int32_t head_dim, int32_t page_size, int32_t num_pages,
+                                int32_t max_blocks, int32_t causal, float softmax_scale, int32_t* status,
+                                void* stream) {
+  using namespace pkv;
+  clear_error();
+  const char* fn = "pkv_prefill_attn";
+  int rc = validate_attn(fn, q, q_sb, q_ss, q_sh, k_new, kn_sb, kn_ss, kn_sh, v_new, vn_sb, vn_ss, vn_sh, k_cache,
+                         v_cache, cache_page_stride, block_table, bt_stride, cache_seqlens, out, o_sb, o_ss, o_sh,
+                         batch, s_q, n_heads, n_kv, head_dim, page_size, num_pages, max_blocks, softmax_scale);
+  if (rc) return rc;
+  const int64_t R = int64_t(s_q) * (n_heads / n_kv);
+  if (R > (int64_t(1) << 30)) return fail(PKV_EINVAL, "%s: too many query rows", fn);
+  if (batch == 0) return PKV_OK;
+  AttnParams p;
+  fill_params(p, q, q_sb, q_ss, q_sh, k_new, kn_sb, kn_ss, kn_sh, v_new, vn_sb, vn_ss, vn_sh, k_cache, v_cache,
+              cache_page_stride, block_table, bt_stride, cache_seqlens, out, o_sb, o_ss, o_sh, s_q, n_heads, n_kv,
+              page_size, num_pages, max_blocks, causal, softmax_scale, status);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (head_dim == 128)
+    launch_prefill_hd<128>(p, batch, s);
+  else
+    launch_prefill_hd<64>(p, batch, s);
+  return check_launch(fn);
+}

@@ -1,0 +1,152 @@
+"""GPU parity of the append + attention kernels against the CPU oracle (through the C ABI).
+
+Bit-exact for the appended cache rows (the whole pools are compared), and the north_star bf16
+tolerance (max-abs <= 1e-2, mean-abs <= 1e-3 against the fp64 oracle rounded to bf16) for outputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+import prism_amd
+from oracle import paged_attention as pa
+from pkv_testutil import assert_attn_close, make_paged_case
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_and_check(gpu, *, batch, ctx, page_size, n_kv, n_heads, head_dim, s_q, causal=True, append=True,
+                   split_tokens=0, seed=0, kernel="auto", extra_cols=0, what=""):
+    cpu, dev = make_paged_case(gpu, batch=batch, ctx=ctx, page_size=page_size, n_kv=n_kv, n_heads=n_heads,
+                               head_dim=head_dim, s_q=s_q, seed=seed, extra_cols=extra_cols)
+    print(f"case {what} B={batch} ctx={list(ctx)[:6]} P={page_size} kv={n_kv} h={n_heads} hd={head_dim} "
+          f"s_q={s_q} causal={causal} append={append} split={split_tokens} kernel={kernel}", flush=True)
+    kw = dict(cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"], causal=causal)
+    k = dev["k"] if append else None
+    v = dev["v"] if append else None
+    if kernel == "prefill":
+        out = prism_amd.prefill_attention(dev["q"], dev["k_cache"], dev["v_cache"], k, v, **kw)
+    else:
+        out = prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], k, v,
+                                                split_tokens=split_tokens, **kw)
+    torch.cuda.synchronize()
+    ref, kb, vb = pa.flash_attn_with_kvcache_ref(
+        cpu["q"], cpu["k_cache"], cpu["v_cache"], cpu["k"] if append else None, cpu["v"] if append else None,
+        cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"], causal=causal)
+    assert np.array_equal(pa.bf16_bits(dev["k_cache"]), kb), "K cache not bit-exact after append"
+    assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "V cache not bit-exact after append"
+    assert_attn_close(out, ref, what)
+    return out
+
+
+DECODE_CASES = [
+    # (batch, ctx, page, n_kv, n_heads, hd, s_q)
+    (4, [1, 300, 1023, 512], 256, 2, 14, 64, 1),          # config-1 shape
+    (3, [0, 255, 256], 256, 4, 28, 128, 1),                # page boundaries, empty cache
+    (5, [31, 32, 33, 63, 64], 16, 4, 28, 128, 1),           # 16-token pages
+    (2, [700, 5], 32, 8, 40, 128, 1),                      # 14B shape
+    (2, [100, 1000], 64, 4, 4, 128, 1),                    # g = 1
+    (3, [517, 2, 90], 256, 4, 28, 128, 5),                 # verify, R = 35
+    (2, [40, 300], 256, 2, 16, 64, 8),                     # R = 64
+    (6, [3000, 17, 4100, 800, 1, 2500], 256, 4, 28, 128, 1),  # ragged, multi-split
+]
+
+
+@pytest.mark.parametrize("case", DECODE_CASES, ids=[f"d{i}" for i in range(len(DECODE_CASES))])
+def test_decode_append_attention(gpu, case):
+    B, ctx, P, n_kv, nh, hd, s_q = case
+    _run_and_check(gpu, batch=B, ctx=ctx, page_size=P, n_kv=n_kv, n_heads=nh, head_dim=hd, s_q=s_q,
+                   what=f"decode{case}")
+
+
+@pytest.mark.parametrize("split", [32, 64, 256, 1 << 20])
+def test_decode_split_invariance(gpu, split):
+    _run_and_check(gpu, batch=3, ctx=[1500, 33, 700], page_size=256, n_kv=4, n_heads=28, head_dim=128, s_q=1,
+                   split_tokens=split, what=f"split{split}")
+
+
+def test_decode_without_append_and_non_causal(gpu):
+    _run_and_check(gpu, batch=3, ctx=[50, 1, 600], page_size=32, n_kv=2, n_heads=14, head_dim=64, s_q=1,
+                   append=False, what="noappend")
+    _run_and_check(gpu, batch=2, ctx=[77, 400], page_size=256, n_kv=4, n_heads=28, head_dim=128, s_q=3,
+                   causal=False, what="noncausal")
+
+
+def test_decode_extra_block_table_columns(gpu):
+    # a wider table than needed (stale columns are never read)
+    _run_and_check(gpu, batch=2, ctx=[10, 300], page_size=256, n_kv=4, n_heads=28, head_dim=128, s_q=1,
+                   extra_cols=5, what="widetable")
+
+
+PREFILL_CASES = [
+    (2, [0, 700], 256, 8, 40, 128, 128),
+    (3, [0, 33, 290], 32, 4, 28, 128, 37),
+    (2, [5, 1000], 256, 2, 14, 64, 100),
+    (1, [0], 256, 4, 4, 128, 300),
+]
+
+
+@pytest.mark.parametrize("case", PREFILL_CASES, ids=[f"p{i}" for i in range(len(PREFILL_CASES))])
+def test_prefill_append_attention(gpu, case):
+    B, ctx, P, n_kv, nh, hd, s_q = case
+    _run_and_check(gpu, batch=B, ctx=ctx, page_size=P, n_kv=n_kv, n_heads=nh, head_dim=hd, s_q=s_q,
+                   what=f"prefill{case}")
+
+
+def test_prefill_kernel_on_small_queries_matches(gpu):
+    # the row-parallel kernel on a decode-sized problem (cross-checks both kernels' indexing)
+    _run_and_check(gpu, batch=3, ctx=[900, 4, 256], page_size=256, n_kv=4, n_heads=28, head_dim=128, s_q=1,
+                   kernel="prefill", what="prefill-s1")
+    _run_and_check(gpu, batch=2, ctx=[90, 513], page_size=256, n_kv=4, n_heads=28, head_dim=128, s_q=5,
+                   kernel="prefill", what="prefill-s5")
+
+
+def test_strided_qkv_views_like_prism(gpu):
+    # engine/executor.py:256-260 passes q/k/v as views into the fused QKV projection output
+    torch.manual_seed(0)
+    B, nh, n_kv, hd, P = 4, 28, 4, 128, 256
+    qs, kvs = nh * hd, n_kv * hd
+    cpu, dev = make_paged_case(gpu, batch=B, ctx=[10, 200, 256, 1000], page_size=P, n_kv=n_kv, n_heads=nh,
+                               head_dim=hd, s_q=1)
+    qkv = torch.randn(B, 1, qs + 2 * kvs, device=gpu).to(torch.bfloat16)
+    q = qkv[:, :, :qs].view(B, 1, nh, hd)
+    k = qkv[:, :, qs:qs + kvs].view(B, 1, n_kv, hd)
+    v = qkv[:, :, qs + kvs:].view(B, 1, n_kv, hd)
+    assert not k.is_contiguous()
+    out = prism_amd.flash_attn_with_kvcache(q, dev["k_cache"], dev["v_cache"], k=k, v=v,
+                                            cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"],
+                                            causal=True)
+    ref, kb, vb = pa.flash_attn_with_kvcache_ref(q.cpu(), cpu["k_cache"], cpu["v_cache"], k.cpu(), v.cpu(),
+                                                 cache_seqlens=cpu["cache_seqlens"],
+                                                 block_table=cpu["block_table"], causal=True)
+    assert np.array_equal(pa.bf16_bits(dev["k_cache"]), kb)
+    assert_attn_close(out, ref, "strided")
+
+
+def test_config1_workload_end_to_end(gpu):
+    from prism_amd import workloads
+
+    w = workloads.config1(gpu, seed=0)
+    kv = w.kv
+    k0, v0 = kv.k_caches[0].cpu(), kv.v_caches[0].cpu()
+    out = prism_amd.flash_attn_with_kvcache(w.q[0], kv.k_caches[0], kv.v_caches[0], k=w.k[0], v=w.v[0],
+                                            cache_seqlens=w.cache_seqlens, block_table=w.block_table, causal=True)
+    torch.cuda.synchronize()
+    ref, kb, vb = pa.flash_attn_with_kvcache_ref(w.q[0].cpu(), k0, v0, w.k[0].cpu(), w.v[0].cpu(),
+                                                 cache_seqlens=w.cache_seqlens.cpu(),
+                                                 block_table=w.block_table.cpu(), causal=True)
+    assert np.array_equal(pa.bf16_bits(kv.k_caches[0]), kb)
+    assert np.array_equal(pa.bf16_bits(kv.v_caches[0]), vb)
+    assert_attn_close(out, ref, "config1")
+
+
+def test_bad_page_id_is_flagged_not_faulted(gpu):
+    # a block-table entry outside the pool is skipped and reported through the status word
+    cpu, dev = make_paged_case(gpu, batch=2, ctx=[40, 300], page_size=256, n_kv=4, n_heads=28, head_dim=128,
+                               s_q=1)
+    bt = dev["block_table"].clone()
+    bt[1, 0] = 10_000
+    st = torch.zeros(1, dtype=torch.int32, device=gpu)
+    prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], dev["k"], dev["v"],
+                                      cache_seqlens=dev["cache_seqlens"], block_table=bt, causal=True, status=st)
+    torch.cuda.synchronize()
+    assert int(st.item()) & 1

@@ -1,0 +1,218 @@
+"""Pins the CPU oracle before anything is checked against it (CPU only).
+
+Each oracle function is checked against something independent of its own formula: worked examples
+in the reference's docs, the documented flash_attn semantics (causal-mask and GQA examples from the
+flash_attn_with_kvcache docstring), torch's SDPA as a library routine, closed forms, and brute
+force.  A plausible slip (top-left causal alignment, h % g head map, missing scale, off-by-one
+slot) fails at least one test here.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_attention as pa
+from oracle import page_ops
+
+
+def _rand_bits(shape, rng):
+    return pa.bf16_bits(torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).to(torch.bfloat16))
+
+
+# ----------------------------------------------------------------------------- slot mapping
+
+def test_slot_mapping_architecture_doc_example():
+    # docs/architecture.md:140-147: block_table[0] = [page_42] holds tokens 0-4 (seqlen 5);
+    # block_table[1] = [page_7, page_13, page_91], seqlen 600: pages 7, 13 full, page 91 has 88.
+    bt = np.array([[42, 0, 0], [7, 13, 91]])
+    s0 = pa.slot_mapping(bt[:1], np.array([0]), 5, 256)
+    assert s0.tolist() == [[42 * 256 + i for i in range(5)]]
+    s1 = pa.slot_mapping(bt[1:], np.array([0]), 600, 256)[0]
+    pages, rows = s1 // 256, s1 % 256
+    assert (pages[:256] == 7).all() and (pages[256:512] == 13).all() and (pages[512:] == 91).all()
+    assert rows[-1] == 87 and (pages == 91).sum() == 88
+    # appending one token to the 600-token sequence lands at page 91, row 88
+    assert pa.slot_mapping(bt[1:], np.array([600]), 1, 256).tolist() == [[91 * 256 + 88]]
+
+
+def test_slot_mapping_hand_values():
+    bt = np.array([[3, 1, 2], [0, 5, 4]])
+    got = pa.slot_mapping(bt, np.array([15, 31]), 2, 16)
+    # seq 0: tokens 15, 16 -> page 3 row 15, page 1 row 0; seq 1: 31, 32 -> page 5 row 15, page 4 row 0
+    assert got.tolist() == [[3 * 16 + 15, 1 * 16 + 0], [5 * 16 + 15, 4 * 16 + 0]]
+
+
+def test_append_vectorised_equals_brute_force():
+    rng = np.random.default_rng(0)
+    P, pages, n_kv, hd = 16, 12, 2, 8
+    k = rng.integers(0, 65535, size=(pages, P, n_kv, hd), dtype=np.uint16)
+    v = rng.integers(0, 65535, size=(pages, P, n_kv, hd), dtype=np.uint16)
+    # disjoint page rows per sequence, shuffled within the row
+    bt = np.arange(12).reshape(3, 4)[:, rng.permutation(4)]
+    sl = np.array([0, 17, 40])
+    kn = rng.integers(0, 65535, size=(3, 7, n_kv, hd), dtype=np.uint16)
+    vn = rng.integers(0, 65535, size=(3, 7, n_kv, hd), dtype=np.uint16)
+    a = pa.append_kv(k, v, kn, vn, bt, sl)
+    b = pa.append_kv_loop(k, v, kn, vn, bt, sl)
+    assert (a[0] == b[0]).all() and (a[1] == b[1]).all()
+    # untouched rows keep their bits
+    changed = (a[0] != k).any(axis=(2, 3))
+    assert changed.sum() <= 3 * 7
+
+
+# ----------------------------------------------------------------------------- attention
+
+def test_causal_mask_flash_attn_docstring_example():
+    # flash_attn_with_kvcache docstring: seqlen_q = 2, seqlen_k = 5, causal mask (1 = keep):
+    #   1 1 1 1 0
+    #   1 1 1 1 1
+    assert pa.causal_visible(2, 5).astype(int).tolist() == [[1, 1, 1, 1, 0], [1, 1, 1, 1, 1]]
+    # and seqlen_q = 5, seqlen_k = 2: rows 0-2 see nothing, row 3 sees key 0, row 4 both
+    assert pa.causal_visible(5, 2).astype(int).tolist() == [[0, 0], [0, 0], [0, 0], [1, 0], [1, 1]]
+
+
+def _paged_from_dense(K, V, P, rng):
+    """Scatter dense [B, L, n_kv, hd] bits into a shuffled page pool; returns pools and table."""
+    B, L, n_kv, hd = K.shape
+    npg = -(-L // P)
+    pool_k = _rand_bits((B * npg + 3, P, n_kv, hd), rng)   # garbage everywhere else
+    pool_v = _rand_bits((B * npg + 3, P, n_kv, hd), rng)
+    perm = rng.permutation(B * npg + 3)
+    bt = perm[: B * npg].reshape(B, npg)
+    for b in range(B):
+        for t in range(L):
+            pool_k[bt[b, t // P], t % P] = K[b, t]
+            pool_v[bt[b, t // P], t % P] = V[b, t]
+    return pool_k, pool_v, bt
+
+
+def test_gqa_head_map_flash_attn_docstring_example():
+    # docstring: Q with 6 heads, K/V with 2: q heads 0,1,2 -> kv head 0; 3,4,5 -> kv head 1.
+    rng = np.random.default_rng(1)
+    L, hd = 9, 8
+    K = _rand_bits((1, L, 2, hd), rng)
+    V = np.zeros((1, L, 2, hd), dtype=np.uint16)
+    V[..., 0, :] = pa.bf16_bits(torch.full((1,), 1.0, dtype=torch.bfloat16))[0]
+    V[..., 1, :] = pa.bf16_bits(torch.full((1,), -2.0, dtype=torch.bfloat16))[0]
+    pk, pv, bt = _paged_from_dense(K, V, 4, rng)
+    q = _rand_bits((1, 1, 6, hd), rng)
+    out = pa.attention_fp64(q, pk, pv, bt, np.array([L]), causal=True)
+    assert np.allclose(out[0, 0, :3], 1.0) and np.allclose(out[0, 0, 3:], -2.0)
+
+
+@pytest.mark.parametrize("nh,n_kv,hd", [(4, 2, 16), (14, 2, 64), (6, 6, 32)])
+def test_attention_matches_sdpa_full_square_causal(nh, n_kv, hd):
+    # s_q == L: bottom-right and top-left alignment coincide, so SDPA(is_causal=True) applies.
+    rng = np.random.default_rng(nh * 100 + hd)
+    B, L, P = 2, 37, 8
+    K = _rand_bits((B, L, n_kv, hd), rng)
+    V = _rand_bits((B, L, n_kv, hd), rng)
+    pk, pv, bt = _paged_from_dense(K, V, P, rng)
+    q = _rand_bits((B, L, nh, hd), rng)
+    out = pa.attention_fp64(q, pk, pv, bt, np.array([L, L]), causal=True)
+    qt = torch.from_numpy(pa.bits_to_f64(q)).transpose(1, 2)
+    kt = torch.from_numpy(pa.bits_to_f64(K)).transpose(1, 2)
+    vt = torch.from_numpy(pa.bits_to_f64(V)).transpose(1, 2)
+    ref = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, is_causal=True, enable_gqa=True)
+    np.testing.assert_allclose(out, ref.transpose(1, 2).numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_attention_matches_sdpa_non_causal_default_scale():
+    rng = np.random.default_rng(7)
+    B, L, P, nh, n_kv, hd = 3, 50, 16, 8, 2, 64
+    K = _rand_bits((B, L, n_kv, hd), rng)
+    V = _rand_bits((B, L, n_kv, hd), rng)
+    pk, pv, bt = _paged_from_dense(K, V, P, rng)
+    q = _rand_bits((B, 3, nh, hd), rng)
+    out = pa.attention_fp64(q, pk, pv, bt, np.array([L] * B), causal=False)
+    qt = torch.from_numpy(pa.bits_to_f64(q)).transpose(1, 2)
+    kt = torch.from_numpy(pa.bits_to_f64(K)).transpose(1, 2)
+    vt = torch.from_numpy(pa.bits_to_f64(V)).transpose(1, 2)
+    ref = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, enable_gqa=True)  # default scale
+    np.testing.assert_allclose(out, ref.transpose(1, 2).numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_closed_forms():
+    rng = np.random.default_rng(3)
+    hd, P = 16, 8
+    # one key: output equals that V row exactly
+    K = _rand_bits((1, 1, 1, hd), rng)
+    V = _rand_bits((1, 1, 1, hd), rng)
+    pk, pv, bt = _paged_from_dense(K, V, P, rng)
+    q = _rand_bits((1, 1, 3, hd), rng)
+    out = pa.attention_fp64(q, pk, pv, bt, np.array([1]), causal=True)
+    assert np.array_equal(out[0, 0], np.repeat(pa.bits_to_f64(V[0, 0]), 3, axis=0))
+    # identical keys: uniform softmax, output = mean of V
+    L = 20
+    K = np.repeat(_rand_bits((1, 1, 1, hd), rng), L, axis=1)
+    V = _rand_bits((1, L, 1, hd), rng)
+    pk, pv, bt = _paged_from_dense(K, V, P, rng)
+    out = pa.attention_fp64(_rand_bits((1, 1, 2, hd), rng), pk, pv, bt, np.array([L]), causal=True)
+    np.testing.assert_allclose(out[0, 0, 0], pa.bits_to_f64(V[0, :, 0]).mean(axis=0), rtol=1e-12, atol=1e-12)
+    # a dominant logit selects its row: key 5 = 8 * q, others 0
+    qv = np.zeros((1, 1, 1, hd), dtype=np.float32)
+    qv[..., 0] = 4.0
+    q = pa.bf16_bits(torch.from_numpy(qv).to(torch.bfloat16))
+    Kf = np.zeros((1, L, 1, hd), dtype=np.float32)
+    Kf[0, 5, 0, 0] = 64.0
+    K = pa.bf16_bits(torch.from_numpy(Kf).to(torch.bfloat16))
+    pk, pv, bt = _paged_from_dense(K, V, P, rng)
+    out = pa.attention_fp64(q, pk, pv, bt, np.array([L]), causal=True)
+    np.testing.assert_allclose(out[0, 0, 0], pa.bits_to_f64(V[0, 5, 0]), atol=1e-20 + 1e-9)
+    # no visible key (s_q > L, causal): zeros
+    out = pa.attention_fp64(_rand_bits((1, 4, 1, hd), rng), pk, pv, bt, np.array([2]), causal=True)
+    assert np.all(out[0, :2] == 0) and np.any(out[0, 3] != 0)
+
+
+def test_scale_argument():
+    rng = np.random.default_rng(5)
+    K = _rand_bits((1, 6, 1, 8), rng)
+    V = _rand_bits((1, 6, 1, 8), rng)
+    pk, pv, bt = _paged_from_dense(K, V, 4, rng)
+    q = _rand_bits((1, 1, 1, 8), rng)
+    a = pa.attention_fp64(q, pk, pv, bt, np.array([6]), causal=False, softmax_scale=0.3)
+    qt = torch.from_numpy(pa.bits_to_f64(q)).transpose(1, 2)
+    kt = torch.from_numpy(pa.bits_to_f64(K)).transpose(1, 2)
+    vt = torch.from_numpy(pa.bits_to_f64(V)).transpose(1, 2)
+    ref = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, scale=0.3)
+    np.testing.assert_allclose(a, ref.transpose(1, 2).numpy(), rtol=1e-10)
+
+
+@pytest.mark.parametrize("s_q,causal", [(1, True), (5, True), (7, False)])
+def test_torch_cpu_path_matches_fp64(s_q, causal):
+    torch.manual_seed(s_q)
+    B, P, n_kv, nh, hd, pages = 3, 16, 2, 6, 32, 20
+    kc = torch.randn(pages, P, n_kv, hd).to(torch.bfloat16)
+    vc = torch.randn(pages, P, n_kv, hd).to(torch.bfloat16)
+    bt = torch.arange(15, dtype=torch.int32).view(3, 5)[:, torch.randperm(5)]
+    sl = torch.tensor([0, 9, 70], dtype=torch.int32)
+    q = torch.randn(B, s_q, nh, hd).to(torch.bfloat16)
+    k = torch.randn(B, s_q, n_kv, hd).to(torch.bfloat16)
+    v = torch.randn(B, s_q, n_kv, hd).to(torch.bfloat16)
+    ref, kb, vb = pa.flash_attn_with_kvcache_ref(q, kc, vc, k, v, cache_seqlens=sl, block_table=bt, causal=causal)
+    kc2, vc2 = kc.clone(), vc.clone()
+    out = pa.flash_attn_cpu(q, kc2, vc2, k, v, cache_seqlens=sl, block_table=bt, causal=causal)
+    assert np.array_equal(pa.bf16_bits(kc2), kb) and np.array_equal(pa.bf16_bits(vc2), vb)
+    np.testing.assert_allclose(out.numpy(), ref, atol=2e-5, rtol=1e-5)
+
+
+# ----------------------------------------------------------------------------- page ops
+
+def test_page_ops_copy_and_compact():
+    rng = np.random.default_rng(9)
+    pools = [rng.integers(0, 65535, size=(10, 4, 2, 8), dtype=np.uint16) for _ in range(3)]
+    dst = [np.zeros_like(p) for p in pools]
+    out = page_ops.copy_pages(pools, dst, [3, 7], [0, 9], fill=[4, 2])
+    for i in range(3):
+        assert (out[i][0] == pools[i][3]).all()
+        assert (out[i][9, :2] == pools[i][7, :2]).all() and (out[i][9, 2:] == 0).all()
+        assert (out[i][1:9] == 0).all()
+    packed, remap = page_ops.compact(pools, [8, 2, 5], 6)
+    assert remap == {8: 0, 2: 1, 5: 2}
+    for i in range(3):
+        for old, new in remap.items():
+            assert (packed[i][new] == pools[i][old]).all()
+        assert (packed[i][3:] == 0).all()
+    t = page_ops.transfer_sequence(pools, dst, [4, 1, 6], [2, 3, 5], seq_len=5, page_size=4)
+    assert (t[0][2] == pools[0][4]).all() and (t[0][3] == pools[0][1]).all() and (t[0][5] == 0).all()
