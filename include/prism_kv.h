@@ -46,6 +46,9 @@ extern "C" {
 
 #define PKV_STATUS_BAD_PAGE 1
 
+/* pkv_decode_attn flags */
+#define PKV_DECODE_TWO_PASS 1 /* merge split-K partials in a second launch instead of in-kernel */
+
 /* ABI version of the loaded library (PKV_ABI_VERSION it was built with). */
 int pkv_abi_version(void);
 
@@ -89,7 +92,13 @@ size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, i
  * 1/sqrt(head_dim)); softmax and accumulation are fp32, out is bf16 [batch, s_q, n_heads,
  * head_dim] with the given strides.  A query row with no visible key gets zeros.
  * split_tokens (multiple of 32, or 0 = library choice) is the KV range one workgroup reduces
- * before the split-K combine.  workspace must hold pkv_decode_workspace_bytes() bytes.
+ * before the split-K merge.  By default the last workgroup of a (sequence, KV head) to finish
+ * merges the partials inside the same launch; flags = PKV_DECODE_TWO_PASS merges them in a
+ * second launch instead (same results up to fp32 rounding order).  workspace must hold pkv_decode_workspace_bytes() bytes and be
+ * zero-filled before its first use; every call leaves it in that state again (its first 64 KiB
+ * hold per-(sequence, KV head) arrival counters, so batch * n_kv <= 16384 when a sequence can
+ * span more than one split).  Calls that share a workspace must be ordered (same
+ * stream).  It may be NULL when pkv_decode_workspace_bytes() returns 0.
  */
 int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
                     const void* k_new, int64_t kn_sb, int64_t kn_ss, int64_t kn_sh,
@@ -100,7 +109,7 @@ int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
                     void* workspace, size_t workspace_bytes,
                     int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv, int32_t head_dim,
                     int32_t page_size, int32_t num_pages, int32_t max_blocks,
-                    int32_t causal, float softmax_scale, int32_t split_tokens,
+                    int32_t causal, float softmax_scale, int32_t split_tokens, int32_t flags,
                     int32_t* status, void* stream);
 
 /*

@@ -19,6 +19,7 @@ PKV_EINVAL = -1
 PKV_EHIP = -2
 PKV_ENOSPC = -3
 PKV_STATUS_BAD_PAGE = 1
+PKV_DECODE_TWO_PASS = 1
 ABI_VERSION = 1
 
 _I64 = c_int64
@@ -49,7 +50,7 @@ _SIGNATURES = {
         _P, c_size_t,                    # workspace
         _I32, _I32, _I32, _I32, _I32,    # batch, s_q, n_heads, n_kv, head_dim
         _I32, _I32, _I32,                # page_size, num_pages, max_blocks
-        _I32, c_float, _I32,             # causal, scale, split_tokens
+        _I32, c_float, _I32, _I32,       # causal, scale, split_tokens, flags
         _P, _P,                          # status, stream
     ]),
     "pkv_prefill_attn": (c_int32, [

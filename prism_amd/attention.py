@@ -30,7 +30,7 @@ from . import _lib
 
 _BF16 = torch.bfloat16
 _ws_lock = threading.Lock()
-_workspaces: dict[int, torch.Tensor] = {}
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
 _status: dict[int, torch.Tensor] = {}
 
 
@@ -64,18 +64,21 @@ def read_status(device: torch.device | str = "cuda", clear: bool = True) -> int:
     return v
 
 
-def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+def _workspace(device: torch.device, nbytes: int, stream: int) -> torch.Tensor | None:
+    """Split-K workspace per (device, stream), grow-only.  Allocated zero-filled: its counter
+    region must start at zero, and every call leaves it zero again."""
     if nbytes == 0:
         return None
     idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, stream)
     with _ws_lock:
-        ws = _workspaces.get(idx)
+        ws = _workspaces.get(key)
         if ws is None or ws.numel() < nbytes:
             if torch.cuda.is_current_stream_capturing():
                 raise RuntimeError(
                     "split-K workspace must be sized by an eager call before HIP graph capture")
-            ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-            _workspaces[idx] = ws
+            ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            _workspaces[key] = ws
         return ws
 
 
@@ -160,6 +163,7 @@ def flash_attn_with_kvcache(
     *,
     out: torch.Tensor | None = None,
     split_tokens: int = 0,
+    two_pass: bool = False,
     status: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Append k/v into the paged cache and attend (see module docstring for the contract).
@@ -167,7 +171,7 @@ def flash_attn_with_kvcache(
     Arguments Prism never passes (rotary_*, cache_batch_idx, cache_leftpad, window_size,
     softcap, alibi_slopes, return_softmax_lse) must keep their defaults.  ``num_splits`` > 0
     fixes the number of KV splits per sequence; ``split_tokens`` > 0 (a multiple of 32) fixes
-    the split length directly.
+    the split length directly; ``two_pass`` merges split-K partials in a second launch.
     """
     if rotary_cos is not None or rotary_sin is not None or cache_batch_idx is not None \
             or cache_leftpad is not None or tuple(window_size) != (-1, -1) or softcap != 0.0 \
@@ -231,7 +235,7 @@ def flash_attn_with_kvcache(
             split_tokens = max(32, -(-per_split // 32) * 32)
         nbytes = lib.pkv_decode_workspace_bytes(batch, s_q, n_heads, n_kv, hd, page_size, max_blocks,
                                                 int(split_tokens))
-        ws = _workspace(device, nbytes)
+        ws = _workspace(device, nbytes, stream)
         rc = lib.pkv_decode_attn(
             q.data_ptr(), *qs, kp, *ks, vp, *vs,
             k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
@@ -239,7 +243,8 @@ def flash_attn_with_kvcache(
             out.data_ptr(), *os_,
             ws.data_ptr() if ws is not None else 0, ws.numel() if ws is not None else 0,
             batch, s_q, n_heads, n_kv, hd, page_size, num_pages, max_blocks,
-            1 if causal else 0, scale, int(split_tokens), st.data_ptr(), stream)
+            1 if causal else 0, scale, int(split_tokens), _lib.PKV_DECODE_TWO_PASS if two_pass else 0,
+            st.data_ptr(), stream)
         _lib.check(rc, "pkv_decode_attn")
     else:
         rc = lib.pkv_prefill_attn(
@@ -254,14 +259,14 @@ def flash_attn_with_kvcache(
 
 
 def decode_attention(q, k_cache, v_cache, k=None, v=None, *, cache_seqlens, block_table,
-                     causal=True, softmax_scale=None, split_tokens=0, out=None, status=None):
+                     causal=True, softmax_scale=None, split_tokens=0, two_pass=False, out=None, status=None):
     """Force the split-K decode kernel (s_q * n_heads / n_kv <= 64)."""
     n_kv = k_cache.shape[2]
     if q.shape[1] * (q.shape[2] // n_kv) > 64:
         raise RuntimeError("decode_attention needs s_q * n_heads / n_kv <= 64")
     return flash_attn_with_kvcache(q, k_cache, v_cache, k, v, cache_seqlens=cache_seqlens,
                                    block_table=block_table, causal=causal, softmax_scale=softmax_scale,
-                                   split_tokens=split_tokens, out=out, status=status)
+                                   split_tokens=split_tokens, two_pass=two_pass, out=out, status=status)
 
 
 def prefill_attention(q, k_cache, v_cache, k=None, v=None, *, cache_seqlens, block_table,

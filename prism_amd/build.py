@@ -32,6 +32,9 @@ HIPCC_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep MFMA accumulators in ordinary VGPRs: the online-softmax rescale touches them from
+    # VALU code, and AGPR homes cost a copy back after every tile (and an occupancy step)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 
@@ -53,15 +56,19 @@ def _run(cmd: list[str]) -> None:
         print(out, file=sys.stderr)
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every csrc/*.hip for gfx950 and link libprism_kv.so.  Always rebuilds."""
+def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
+    """Compile every csrc/*.hip for gfx950 and link libprism_kv.so.  Always rebuilds.
+
+    extra_flags (or the whitespace-separated PKV_HIPCC_FLAGS environment variable) are appended
+    to every compile, e.g. -DPKV_DECODE_DEPTH=1 to build a tuning variant."""
     hipcc = _hipcc()
+    extra = list(extra_flags or []) + os.environ.get("PKV_HIPCC_FLAGS", "").split()
     BUILD_DIR.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     objs = [BUILD_DIR / (s.stem + ".o") for s in sources]
-    cmds = [[hipcc, *HIPCC_FLAGS, "-c", str(s), "-o", str(o)] for s, o in zip(sources, objs)]
+    cmds = [[hipcc, *HIPCC_FLAGS, *extra, "-c", str(s), "-o", str(o)] for s, o in zip(sources, objs)]
     workers = min(len(cmds), max(1, (os.cpu_count() or 2) // 2), 8)
     with cf.ThreadPoolExecutor(workers) as ex:
         for cmd, fut in zip(cmds, [ex.submit(_run, c) for c in cmds]):

@@ -44,23 +44,28 @@ struct AttnParams {
   int64_t o_sb, o_ss, o_sh;
   float* ws_o;   // [batch, n_kv, max_splits, R, head_dim] unnormalised split partials
   float* ws_ml;  // [batch, n_kv, max_splits, R, 2] (row max in log2 units, row sum of exp2)
+  int32_t* ws_cnt;  // [batch, n_kv] split arrival counters, zero between calls
   int32_t* status;
-  int s_q, g, R, n_kv, log2_page, num_pages, max_blocks, split_tokens, max_splits;
-  int causal, has_new;
+  int batch, s_q, g, R, n_kv, log2_page, num_pages, max_blocks, split_tokens, max_splits;
+  int causal, has_new, two_pass;
   float scale_log2;  // softmax_scale * log2(e)
 };
 
+// Reductions over the four lanes {l, l^16, l^32, l^48} that hold the same query row, with the
+// gfx950 row-swap permutes: permlane16_swap(x, x) hands lane l the pair {x[l], x[l^16]} and
+// permlane32_swap(x, x) the pair {x[l], x[l^32]} (no LDS round trip, unlike ds_bpermute).
 __device__ __forceinline__ float max_over_quads(float v) {
-  // max over the four lanes {l, l^16, l^32, l^48} that hold the same query row.
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  v = fmaxf(v, __shfl_xor(v, 32, 64));
-  return v;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 __device__ __forceinline__ float sum_over_quads(float v) {
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -100,29 +105,66 @@ __device__ __forceinline__ int num_splits(const AttnParams& p, int L) {
   return min(n, p.max_splits);
 }
 
+// Split count of a sequence from its raw cache length (same clamping as seq_lengths).
+__device__ __forceinline__ int splits_of(const AttnParams& p, int c_raw) {
+  const int cap = p.max_blocks << p.log2_page;
+  const int c = min(max(c_raw, 0), cap);
+  const int L = min(c + (p.has_new ? p.s_q : 0), cap);
+  return num_splits(p, L);
+}
+
+// Map dense slot j (0-based over every (sequence, split) pair, sequence-major) to (b, split) with
+// a 64-lane prefix scan over the sequences' split counts; false when j is past the last pair.
+// Every lane of the wave gets the same answer.
+__device__ __forceinline__ bool locate_item(const AttnParams& p, int batch, int j, int& b, int& split) {
+  const int lane = threadIdx.x & 63;
+  int base = 0;
+  for (int b0 = 0; b0 < batch; b0 += 64) {
+    const int bb = b0 + lane;
+    const int nb = bb < batch ? splits_of(p, p.seqlens[bb]) : 0;
+    int incl = nb;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += t;
+    }
+    const int total = __shfl(incl, 63, 64);
+    if (j < base + total) {
+      const unsigned long long hit = __ballot(base + incl > j);
+      const int first = __ffsll(static_cast<long long>(hit)) - 1;
+      b = b0 + first;
+      split = j - base - __shfl(incl - nb, first, 64);
+      return true;
+    }
+    base += total;
+  }
+  return false;
+}
+
 // Per-(sequence, KV head) view used by the wave routine.
 struct SeqView {
   int b, h, c, t_end;
   const int32_t* bt;
 };
 
-// Address of the head-h row of token t, or nullptr when t is out of range or its page id is
-// bad.  Rows being appended by this call (t >= c) come straight from k_new / v_new, so no
-// workgroup ever reads a cache slot that the same call writes.
-__device__ __forceinline__ const uint16_t* kv_row(const AttnParams& p, const SeqView& sv, bool is_v, int t,
-                                                  int pid, int hd) {
-  if (t >= sv.t_end) return nullptr;
-  if (p.has_new && t >= sv.c) {
-    const int j = t - sv.c;
-    return is_v ? p.v_new + sv.b * p.vn_sb + j * p.vn_ss + sv.h * p.vn_sh
-                : p.k_new + sv.b * p.kn_sb + j * p.kn_ss + sv.h * p.kn_sh;
-  }
-  if (pid < 0 || pid >= p.num_pages) {
-    flag_status(p.status, PKV_STATUS_BAD_PAGE);
-    return nullptr;
-  }
-  return (is_v ? p.v_cache : p.k_cache) + int64_t(pid) * p.page_stride +
-         int64_t(t & ((1 << p.log2_page) - 1)) * (p.n_kv * hd) + sv.h * hd;
+// Block-table window of one wave: lane l holds block_table[b, col0 + l] (or -1 past max_blocks),
+// so the page of a tile is one v_readlane away instead of a memory round trip per tile.
+struct BtWindow {
+  int col0;
+  int ids;
+};
+
+__device__ __forceinline__ void bt_window_load(const AttnParams& p, const SeqView& sv, int col0, BtWindow& w) {
+  const int lane = threadIdx.x & 63;
+  const int col = col0 + lane;
+  w.col0 = col0;
+  w.ids = col < p.max_blocks ? sv.bt[col] : -1;
+}
+
+// Page id of block-table column `col` (uniform); refills the window when col leaves it.
+__device__ __forceinline__ int bt_page(const AttnParams& p, const SeqView& sv, int col, BtWindow& w) {
+  if (col - w.col0 >= 64 || col < w.col0) bt_window_load(p, sv, col, w);
+  return __builtin_amdgcn_readlane(w.ids, col - w.col0);
 }
 
 // Load the Q^T operand for the 16*NT rows starting at row0 and the last key each row may see.
@@ -151,83 +193,158 @@ __device__ __forceinline__ void load_q(const AttnParams& p, const SeqView& sv, i
   }
 }
 
-// Online-softmax attention of one wave's 16*NT query rows over the 32-token tiles starting at
-// token T_first, T_step apart, below T_stop.  Accumulates into (m_run, l_run, acc); l_run is a
-// per-lane partial (sum over the lane's own tokens) to be reduced with sum_over_quads.
+// A pointer the whole wave agrees on, pinned to scalar registers.
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* ptr) {
+  const uint64_t a = reinterpret_cast<uint64_t>(ptr);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(a >> 32));
+  return reinterpret_cast<T*>((uint64_t(hi) << 32) | lo);
+}
+
+// Registers of one 32-token tile: the K rows of both QK MFMA groups and the V slices.
+template <int HD>
+struct KVTile {
+  u32x4 kr[2][HD / 32];
+  VRow<HD> vr[8];
+};
+
+// Per-lane constant byte offsets of the K and V slices a lane loads, relative to the tile's
+// first row (token T0) of head h in its page: valid for every tile that lies in one page.
+struct LaneOffsets {
+  uint32_t k[2];  // K row of QK group a, + 64 * kk bytes per 32-element chunk
+  uint32_t v;     // V row of token 8lq (token 8lq + e is e * row_bytes further)
+};
+
+template <int HD>
+__device__ __forceinline__ LaneOffsets lane_offsets(const AttnParams& p) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15;
+  const int lq = lane >> 4;
+  const uint32_t row_elems = uint32_t(p.n_kv * HD);
+  LaneOffsets o;
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+    const uint32_t tt = 8 * (li >> 2) + 4 * a + (li & 3);
+    o.k[a] = (tt * row_elems + 8 * lq) * 2u;
+  }
+  o.v = ((8 * lq) * row_elems + (HD / 16) * li) * 2u;
+  return o;
+}
+
+// Issue every load of the tile at token T0 (uniform) into tl.  Every row is read from the cache
+// (rows appended by this call were written before the tile loop).  Addressing is a per-tile base
+// plus constant per-lane offsets; rows of the half after token T0 + 16 use a second base, which
+// differs from the first only for 16-row pages.  V rows past t_end (only in the last tile) are
+// zeroed, since P = 0 times a stale NaN would still poison the PV product; K rows past t_end need
+// nothing, their scores are masked.  A page id outside the pool is flagged and read as page 0.
+template <int HD>
+__device__ __forceinline__ void load_tile(const AttnParams& p, const SeqView& sv, int T0, BtWindow& btw,
+                                          const LaneOffsets& lo, KVTile<HD>& tl) {
+  constexpr int KK = HD / 32;
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15;
+  const int lq = lane >> 4;
+  const int row_elems = p.n_kv * HD;
+  const int pmask = (1 << p.log2_page) - 1;
+  const int pidA = bt_page(p, sv, T0 >> p.log2_page, btw);
+  const bool okA = unsigned(pidA) < unsigned(p.num_pages);
+  if (!okA && T0 < sv.t_end) flag_status(p.status, PKV_STATUS_BAD_PAGE);
+  const int64_t offA = int64_t(okA ? pidA : 0) * p.page_stride + int64_t(T0 & pmask) * row_elems + sv.h * HD;
+  if (p.log2_page >= 5) {
+    // scalar bases + 32-bit per-lane offsets: global_load ... voffset, saddr
+    const char* kb = uniform_ptr(reinterpret_cast<const char*>(p.k_cache + offA));
+    const char* vb = uniform_ptr(reinterpret_cast<const char*>(p.v_cache + offA));
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) tl.kr[a][kk] = ld16(kb + (lo.k[a] + 64 * kk));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const char* vbe = uniform_ptr(vb + int64_t(e) * row_elems * 2);
+      load_vrow<HD>(tl.vr[e], reinterpret_cast<const uint16_t*>(vbe + lo.v));
+    }
+  } else {
+    // 16-row pages: the tile's second half lives on the next page
+    const int pidB = bt_page(p, sv, (T0 + 16) >> p.log2_page, btw);
+    const bool okB = unsigned(pidB) < unsigned(p.num_pages);
+    if (!okB && T0 + 16 < sv.t_end) flag_status(p.status, PKV_STATUS_BAD_PAGE);
+    const int64_t offB = int64_t(okB ? pidB : 0) * p.page_stride - 16 * int64_t(row_elems) + sv.h * HD;
+    const char* kb = reinterpret_cast<const char*>(p.k_cache + (li >= 8 ? offB : offA));
+    const char* vb = reinterpret_cast<const char*>(p.v_cache + (lq >= 2 ? offB : offA));
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) tl.kr[a][kk] = ld16(kb + lo.k[a] + 64 * kk);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      load_vrow<HD>(tl.vr[e], reinterpret_cast<const uint16_t*>(vb + uint32_t(e * row_elems * 2) + lo.v));
+  }
+  if (T0 + 32 > sv.t_end) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool keep = T0 + 8 * lq + e < sv.t_end;
+#pragma unroll
+      for (int w = 0; w < HD / 32; ++w) tl.vr[e].w[w] = keep ? tl.vr[e].w[w] : 0u;
+    }
+  }
+}
+
+// Rows rescale their output only when their running max grows by more than this (log2 units),
+// so exp2 arguments stay <= kRescaleSlack and P <= 2^kRescaleSlack: the rescale of the MFMA
+// accumulators becomes a rare, wave-uniform branch instead of work on every tile.
+constexpr float kRescaleSlack = 8.0f;
+#ifndef PKV_DECODE_DEPTH
+#define PKV_DECODE_DEPTH 2
+#endif
+#ifndef PKV_PREFILL_DEPTH
+#define PKV_PREFILL_DEPTH 1
+#endif
+constexpr int kDecodeDepth = PKV_DECODE_DEPTH;
+constexpr int kPrefillDepth = PKV_PREFILL_DEPTH;
+
+// Online-softmax update of one wave's 16*NT query rows with the tile at token T0.
 // SPLIT_P feeds P to the PV MFMA as a bf16 hi + lo pair (two MFMAs) instead of one bf16
 // rounding: decode has an order of magnitude of MFMA headroom, and short contexts then keep the
 // output error down to the output's own bf16 rounding.
 template <int HD, int NT, bool SPLIT_P>
-__device__ __forceinline__ void wave_attend(const AttnParams& p, const SeqView& sv, const bf16x8 (&qf)[NT][HD / 32],
-                                            const int (&lim)[NT], int T_first, int T_stop, int T_step,
-                                            float (&m_run)[NT], float (&l_run)[NT], f32x4 (&acc)[NT][HD / 16]) {
+__device__ __forceinline__ void compute_tile(const AttnParams& p, const KVTile<HD>& tl, int T0,
+                                             const bf16x8 (&qf)[NT][HD / 32], const int (&lim)[NT], int lim_min,
+                                             float (&m_run)[NT], float (&l_run)[NT], f32x4 (&acc)[NT][HD / 16]) {
   constexpr int KK = HD / 32;
   constexpr int DPL = HD / 16;
   const int lane = threadIdx.x & 63;
-  const int li = lane & 15;
   const int lq = lane >> 4;
 
-  for (int T0 = T_first; T0 < T_stop; T0 += T_step) {
-    // Page of each 16-token half (the same page whenever page_size >= 32).
-    const int colA = T0 >> p.log2_page;
-    const int colB = (T0 + 16) >> p.log2_page;
-    const int pidA = colA < p.max_blocks ? sv.bt[colA] : -1;
-    const int pidB = colB < p.max_blocks ? sv.bt[colB] : -1;
+  // V^T operands: PV MFMA n covers head-dim elements d = DPL*i + n (i = M row = lane li);
+  // element e of the operand is token T0 + 8lq + e.
+  bf16x8 vt[DPL];
+#pragma unroll
+  for (int n = 0; n < DPL; ++n) {
+    const int w = n >> 1;
+    const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
+    u32x4 pk;
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) pk[pp] = __builtin_amdgcn_perm(tl.vr[2 * pp + 1].w[w], tl.vr[2 * pp].w[w], sel);
+    vt[n] = __builtin_bit_cast(bf16x8, pk);
+  }
 
-    // K: lane (li, lq) supplies M-row li of QK tile a = token T0 + 8*(li/4) + 4a + li%4 and
-    // head-row elements [32kk + 8lq, +8).
-    u32x4 kr[2][KK];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    f32x4 s[2];
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
-      const int tt = 8 * (li >> 2) + 4 * a + (li & 3);
-      const uint16_t* kp = kv_row(p, sv, false, T0 + tt, tt < 16 ? pidA : pidB, HD);
+      s[a] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) kr[a][kk] = kp ? ld16(kp + 32 * kk + 8 * lq) : u32x4{0u, 0u, 0u, 0u};
+      for (int kk = 0; kk < KK; ++kk)
+        s[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, tl.kr[a][kk]), qf[nt][kk], s[a],
+                                                      0, 0, 0);
     }
-    // V: lane (li, lq) loads tokens T0 + 8lq + e (e < 8), head-row elements [DPL*li, +DPL).
-    VRow<HD> vr[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int tt = 8 * lq + e;
-      const uint16_t* vp = kv_row(p, sv, true, T0 + tt, tt < 16 ? pidA : pidB, HD);
-      if (vp) {
-        load_vrow<HD>(vr[e], vp + DPL * li);
-      } else {
-#pragma unroll
-        for (int w = 0; w < HD / 32; ++w) vr[e].w[w] = 0u;
-      }
-    }
-
-    // V^T operands: PV MFMA n covers head-dim elements d = DPL*i + n (i = M row = lane li);
-    // element e of the operand is token T0 + 8lq + e.
-    bf16x8 vt[DPL];
-#pragma unroll
-    for (int n = 0; n < DPL; ++n) {
-      const int w = n >> 1;
-      u32x4 pk;
-#pragma unroll
-      for (int pp = 0; pp < 4; ++pp) {
-        const uint32_t x0 = vr[2 * pp].w[w];
-        const uint32_t x1 = vr[2 * pp + 1].w[w];
-        pk[pp] = (n & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
-      }
-      vt[n] = __builtin_bit_cast(bf16x8, pk);
-    }
-
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      f32x4 s[2];
-#pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        s[a] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk)
-          s[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[a][kk]), qf[nt][kk], s[a],
-                                                        0, 0, 0);
-      }
-      // s[a][r]: score of token T0 + 8lq + 4a + r against query row li + 16nt.
-      float x[8];
-      float mx = -INFINITY;
+    // s[a][r]: score of token T0 + 8lq + 4a + r against query row li + 16nt.  Only tiles that
+    // reach past some real row's last visible key pay for the mask (a wave-uniform test).
+    float x[8];
+    float mx = -INFINITY;
+    if (T0 + 31 > lim_min) {
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
 #pragma unroll
@@ -238,36 +355,97 @@ __device__ __forceinline__ void wave_attend(const AttnParams& p, const SeqView& 
           mx = fmaxf(mx, v);
         }
       }
-      mx = max_over_quads(mx);
-      const float m_new = fmaxf(m_run[nt], mx);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run[nt] - m_use);
-      float psum = 0.f;
-      u32x4 pk, pk_lo;
+    } else {
 #pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const float p0 = fast_exp2(x[e] - m_use);
-        const float p1 = fast_exp2(x[e + 1] - m_use);
-        psum += p0 + p1;
-        pk[e >> 1] = pack_bf16x2(p0, p1);
-        if constexpr (SPLIT_P) {
-          // P = hi + lo with both halves bf16: the PV product then carries ~16 mantissa bits of P
-          const float h0 = bf16_bits_to_f32(pk[e >> 1] & 0xffffu);
-          const float h1 = bf16_bits_to_f32(pk[e >> 1] >> 16);
-          pk_lo[e >> 1] = pack_bf16x2(p0 - h0, p1 - h1);
+      for (int a = 0; a < 2; ++a) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          x[4 * a + r] = s[a][r] * p.scale_log2;
+          mx = fmaxf(mx, x[4 * a + r]);
         }
       }
-      l_run[nt] = l_run[nt] * alpha + psum;
-      m_run[nt] = m_new;
-      const bf16x8 pb = __builtin_bit_cast(bf16x8, pk);
+    }
+    mx = max_over_quads(mx);
+    const bool grow = mx > m_run[nt] + kRescaleSlack;
+    if (__any(grow)) {
+      const float m_new = grow ? mx : m_run[nt];
+      const float alpha = fast_exp2(m_run[nt] - m_new);  // 0 on the first visible tile, 1 if unchanged
+      l_run[nt] *= alpha;
 #pragma unroll
-      for (int n = 0; n < DPL; ++n) {
-        acc[nt][n] *= alpha;
-        acc[nt][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[n], pb, acc[nt][n], 0, 0, 0);
-        if constexpr (SPLIT_P)
-          acc[nt][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[n], __builtin_bit_cast(bf16x8, pk_lo),
-                                                              acc[nt][n], 0, 0, 0);
+      for (int n = 0; n < DPL; ++n) acc[nt][n] *= alpha;
+      m_run[nt] = m_new;
+    }
+    const float m_use = (m_run[nt] == -INFINITY) ? 0.f : m_run[nt];
+    float psum = 0.f;
+    u32x4 pk, pk_lo;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const float p0 = fast_exp2(x[e] - m_use);
+      const float p1 = fast_exp2(x[e + 1] - m_use);
+      psum += p0 + p1;
+      pk[e >> 1] = pack_bf16x2(p0, p1);
+      if constexpr (SPLIT_P) {
+        const float h0 = bf16_bits_to_f32(pk[e >> 1] & 0xffffu);
+        const float h1 = bf16_bits_to_f32(pk[e >> 1] >> 16);
+        pk_lo[e >> 1] = pack_bf16x2(p0 - h0, p1 - h1);
       }
+    }
+    l_run[nt] += psum;
+    const bf16x8 pb = __builtin_bit_cast(bf16x8, pk);
+#pragma unroll
+    for (int n = 0; n < DPL; ++n) {
+      acc[nt][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[n], pb, acc[nt][n], 0, 0, 0);
+      if constexpr (SPLIT_P)
+        acc[nt][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[n], __builtin_bit_cast(bf16x8, pk_lo), acc[nt][n],
+                                                            0, 0, 0);
+    }
+  }
+}
+
+// Online-softmax attention of one wave's 16*NT query rows over the 32-token tiles starting at
+// token T_first (uniform), T_step apart, below T_stop.  With DEPTH = 2, two register tiles
+// alternate so the loads of tile i+1 are in flight while tile i is computed.  m_run is the
+// row's softmax reference (within kRescaleSlack of its running max); l_run is a per-lane partial
+// (sum over the lane's own tokens) to be reduced with sum_over_quads.
+template <int HD, int NT, bool SPLIT_P, int DEPTH>
+__device__ __forceinline__ void wave_attend(const AttnParams& p, const SeqView& sv, const bf16x8 (&qf)[NT][HD / 32],
+                                            const int (&lim)[NT], int T_first, int T_stop, int T_step,
+                                            float (&m_run)[NT], float (&l_run)[NT], f32x4 (&acc)[NT][HD / 16]) {
+  int T0 = __builtin_amdgcn_readfirstlane(T_first);
+  T_stop = __builtin_amdgcn_readfirstlane(T_stop);
+  T_step = __builtin_amdgcn_readfirstlane(T_step);
+  if (T0 >= T_stop) return;
+  const LaneOffsets lo = lane_offsets<HD>(p);
+  // smallest last-visible key over the wave's real rows (padding rows have lim = -1 and never
+  // reach the output, so they are left out)
+  int lim_min = 0x7fffffff;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) lim_min = min(lim_min, lim[nt] < 0 ? 0x7fffffff : lim[nt]);
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) lim_min = min(lim_min, __shfl_xor(lim_min, off, 64));
+  lim_min = __builtin_amdgcn_readfirstlane(lim_min);
+  (void)lane;
+  BtWindow btw;
+  bt_window_load(p, sv, T0 >> p.log2_page, btw);
+  if constexpr (DEPTH == 1) {
+    for (; T0 < T_stop; T0 += T_step) {
+      KVTile<HD> t0;
+      load_tile<HD>(p, sv, T0, btw, lo, t0);
+      compute_tile<HD, NT, SPLIT_P>(p, t0, T0, qf, lim, lim_min, m_run, l_run, acc);
+    }
+  } else {
+    KVTile<HD> t0, t1;
+    load_tile<HD>(p, sv, T0, btw, lo, t0);
+    for (;;) {
+      int T1 = T0 + T_step;
+      if (T1 < T_stop) load_tile<HD>(p, sv, T1, btw, lo, t1);
+      compute_tile<HD, NT, SPLIT_P>(p, t0, T0, qf, lim, lim_min, m_run, l_run, acc);
+      if (T1 >= T_stop) break;
+      T0 = T1 + T_step;
+      if (T0 < T_stop) load_tile<HD>(p, sv, T0, btw, lo, t0);
+      compute_tile<HD, NT, SPLIT_P>(p, t1, T1, qf, lim, lim_min, m_run, l_run, acc);
+      if (T0 >= T_stop) break;
     }
   }
 }
@@ -310,13 +488,77 @@ __device__ __forceinline__ void store_out_row8(const AttnParams& p, int b, int h
   st16(p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + d0, ov);
 }
 
+// Split partials cross workgroups that may run on different XCDs, whose L2s are not coherent
+// with each other.  They are written and read with agent-scope relaxed atomics, which gfx950
+// issues as plain global_store / global_load with the sc1 bit (coherent at device scope), so no
+// L2-wide writeback or invalidate is needed anywhere in the protocol.
+__device__ __forceinline__ void st_coherent(float* ptr, float v) {
+  __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coherent(const float* ptr) {
+  return __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Log-sum-exp merge of the n_split partials of (b, h) into the bf16 output, by `nthreads` threads.
+// Splits are merged kMergeChunk at a time with every load of a chunk issued before any is used,
+// so the merge costs one memory round trip per chunk rather than one per split.
+constexpr int kMergeChunk = 4;
+
+template <int HD>
+__device__ __forceinline__ void combine_splits(const AttnParams& p, int b, int h, int n_split, int tid, int nthreads) {
+  constexpr int CPR = HD / 8;
+  for (int idx = tid; idx < p.R * CPR; idx += nthreads) {
+    const int row = idx / CPR;
+    const int d0 = (idx - row * CPR) * 8;
+    const int64_t base = int64_t(b * p.n_kv + h) * p.max_splits * p.R + row;
+    float M = -INFINITY;
+    float lsum = 0.f;
+    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < n_split; s0 += kMergeChunk) {
+      float m[kMergeChunk], l[kMergeChunk], x[kMergeChunk][8];
+#pragma unroll
+      for (int u = 0; u < kMergeChunk; ++u) {
+        const int64_t slot = base + int64_t(min(s0 + u, n_split - 1)) * p.R;
+        m[u] = ld_coherent(p.ws_ml + slot * 2);
+        l[u] = ld_coherent(p.ws_ml + slot * 2 + 1);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[u][k] = ld_coherent(p.ws_o + slot * HD + d0 + k);
+      }
+      float Mc = M;
+#pragma unroll
+      for (int u = 0; u < kMergeChunk; ++u)
+        if (s0 + u < n_split) Mc = fmaxf(Mc, m[u]);
+      const float M_use = (Mc == -INFINITY) ? 0.f : Mc;
+      const float f_old = fast_exp2(M - M_use);
+      lsum *= f_old;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) o[k] *= f_old;
+#pragma unroll
+      for (int u = 0; u < kMergeChunk; ++u) {
+        const float f = (s0 + u < n_split) ? fast_exp2(m[u] - M_use) : 0.f;
+        lsum += f * l[u];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o[k] += f * x[u][k];
+      }
+      M = Mc;
+    }
+    store_out_row8(p, b, h, row, d0, o, lsum);
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // Decode / verify: grid (split, KV head, sequence).  The W waves take interleaved 32-token tiles
 // of the split and merge (m, l, O) through LDS.  A sequence whose keys fit one split writes the
-// bf16 output directly; otherwise the split writes its partial for combine_kernel.
+// bf16 output directly.  Otherwise each split writes its partial to the workspace and bumps the
+// (b, h) arrival counter; the last split to arrive merges all partials and writes the output, and
+// resets the counter to zero for the next call.  One launch per call, no separate combine pass.
 // ---------------------------------------------------------------------------------------------
+#ifndef PKV_DECODE_MIN_BLOCKS
+#define PKV_DECODE_MIN_BLOCKS 1
+#endif
+
 template <int HD, int NT, int W>
-__global__ __launch_bounds__(64 * W) void decode_kernel(const AttnParams p) {
+__global__ __launch_bounds__(64 * W, PKV_DECODE_MIN_BLOCKS) void decode_kernel(const AttnParams p) {
   constexpr int DPL = HD / 16;
   constexpr int ROWS = 16 * NT;
   constexpr int CPR = HD / 8;
@@ -324,19 +566,21 @@ __global__ __launch_bounds__(64 * W) void decode_kernel(const AttnParams p) {
   __shared__ float sm_o[W][ROWS][HD + 4];
   __shared__ float sm_m[W][ROWS];
   __shared__ float sm_l[W][ROWS];
+  __shared__ int sm_last;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int li = lane & 15;
   const int lq = lane >> 4;
-  const int split = blockIdx.x;
-  const int h = blockIdx.y;
-  const int b = blockIdx.z;
+  // Dense work numbering: item = ((sequence, split) slot) * n_kv + head, so the real work fills
+  // the front of the 1-D grid and consecutive items land on different XCDs.
+  const int h = blockIdx.x % p.n_kv;
+  int b, split;
+  if (!locate_item(p, p.batch, blockIdx.x / p.n_kv, b, split)) return;
 
   int c, L;
   seq_lengths(p, b, c, L);
   const int t_begin = split * p.split_tokens;
-  if (split > 0 && t_begin >= L) return;
   const int n_split_b = num_splits(p, L);
   SeqView sv;
   sv.b = b;
@@ -345,7 +589,12 @@ __global__ __launch_bounds__(64 * W) void decode_kernel(const AttnParams p) {
   sv.t_end = min(t_begin + p.split_tokens, L);
   sv.bt = p.block_table + int64_t(b) * p.bt_stride;
 
-  if (p.has_new) append_rows<HD>(p, sv, max(max(c, t_begin), 0), sv.t_end, threadIdx.x, 64 * W);
+  // Append the new rows that fall in this split.  Only this workgroup reads them, after the
+  // barrier: its waves share one CU and its L1, so the stores are visible to their loads.
+  if (p.has_new) {
+    append_rows<HD>(p, sv, max(max(c, t_begin), 0), sv.t_end, threadIdx.x, 64 * W);
+    __syncthreads();
+  }
 
   bf16x8 qf[NT][HD / 32];
   int lim[NT];
@@ -361,7 +610,8 @@ __global__ __launch_bounds__(64 * W) void decode_kernel(const AttnParams p) {
     for (int n = 0; n < DPL; ++n) acc[nt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   // The last query row (j = s_q - 1) sees every key of the split, so the whole split is walked.
-  wave_attend<HD, NT, true>(p, sv, qf, lim, t_begin + 32 * wave, sv.t_end, 32 * W, m_run, l_run, acc);
+  wave_attend<HD, NT, true, kDecodeDepth>(p, sv, qf, lim, t_begin + 32 * wave, sv.t_end, 32 * W, m_run, l_run,
+                                         acc);
 
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
@@ -400,57 +650,48 @@ __global__ __launch_bounds__(64 * W) void decode_kernel(const AttnParams p) {
     } else {
       const int64_t slot = (int64_t(b * p.n_kv + h) * p.max_splits + split) * p.R + row;
       float* dst = p.ws_o + slot * HD + d0;
-      *reinterpret_cast<f32x4*>(dst) = f32x4{o[0], o[1], o[2], o[3]};
-      *reinterpret_cast<f32x4*>(dst + 4) = f32x4{o[4], o[5], o[6], o[7]};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) st_coherent(dst + k, o[k]);
       if (d0 == 0) {
-        p.ws_ml[slot * 2] = M;
-        p.ws_ml[slot * 2 + 1] = lsum;
+        st_coherent(p.ws_ml + slot * 2, M);
+        st_coherent(p.ws_ml + slot * 2 + 1, lsum);
       }
     }
   }
+  if (n_split_b == 1 || p.two_pass) return;
+
+  // Count this split's arrival once all of its partial stores have completed; the last split
+  // of (b, h) to arrive merges every partial and re-arms the counter for the next call.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = atomicAdd(p.ws_cnt + (b * p.n_kv + h), 1);
+    sm_last = (prev == n_split_b - 1);
+  }
+  __syncthreads();
+  if (!sm_last) return;
+  combine_splits<HD>(p, b, h, n_split_b, threadIdx.x, 64 * W);
+  if (threadIdx.x == 0) __hip_atomic_store(p.ws_cnt + (b * p.n_kv + h), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Log-sum-exp combine of the split partials of every (sequence, KV head) with > 1 split.
+// Two-pass mode: the split-K merge as its own launch (kernel boundaries order everything).
 template <int HD>
 __global__ __launch_bounds__(256) void combine_kernel(const AttnParams p) {
-  constexpr int CPR = HD / 8;
   const int h = blockIdx.y;
   const int b = blockIdx.z;
   int c, L;
   seq_lengths(p, b, c, L);
   const int n_split_b = num_splits(p, L);
   if (n_split_b <= 1) return;
-  const int idx = blockIdx.x * 256 + threadIdx.x;
-  if (idx >= p.R * CPR) return;
-  const int row = idx / CPR;
-  const int d0 = (idx - row * CPR) * 8;
-  const int64_t base = int64_t(b * p.n_kv + h) * p.max_splits * p.R + row;
-  float M = -INFINITY;
-  for (int s = 0; s < n_split_b; ++s) M = fmaxf(M, p.ws_ml[(base + int64_t(s) * p.R) * 2]);
-  const float M_use = (M == -INFINITY) ? 0.f : M;
-  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float lsum = 0.f;
-  for (int s = 0; s < n_split_b; ++s) {
-    const int64_t slot = base + int64_t(s) * p.R;
-    const float f = fast_exp2(p.ws_ml[slot * 2] - M_use);
-    lsum += f * p.ws_ml[slot * 2 + 1];
-    const f32x4 x0 = *reinterpret_cast<const f32x4*>(p.ws_o + slot * HD + d0);
-    const f32x4 x1 = *reinterpret_cast<const f32x4*>(p.ws_o + slot * HD + d0 + 4);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      o[k] += f * x0[k];
-      o[4 + k] += f * x1[k];
-    }
-  }
-  store_out_row8(p, b, h, row, d0, o, lsum);
+  combine_splits<HD>(p, b, h, n_split_b, threadIdx.x, 256);
 }
 
 // ---------------------------------------------------------------------------------------------
 // Prefill: grid (row tile, KV head, sequence).  Each wave owns 16*NT consecutive query rows and
 // walks every KV tile its rows can see (causal: up to the wave's last visible key); the W waves
 // of a workgroup read the same tiles at about the same time, so the second and later reads hit
-// the CU's L1.  No split-K: each wave normalises and writes its own rows.  Row tile 0 appends
-// the new rows of (b, h) to the cache; reads of those rows go to k_new / v_new.
+// the CU's L1.  No split-K: each wave normalises and writes its own rows.  The new rows were
+// appended to the cache by a preceding append launch, so every key is read from the cache.
 // ---------------------------------------------------------------------------------------------
 template <int HD, int NT, int W>
 __global__ __launch_bounds__(64 * W) void prefill_kernel(const AttnParams p) {
@@ -471,8 +712,6 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(const AttnParams p) {
   sv.t_end = L;
   sv.bt = p.block_table + int64_t(b) * p.bt_stride;
 
-  if (p.has_new && blockIdx.x == 0) append_rows<HD>(p, sv, max(c, 0), L, threadIdx.x, 64 * W);
-
   const int row0 = (blockIdx.x * W + wave) * 16 * NT;
   if (row0 >= p.R) return;
 
@@ -492,7 +731,7 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(const AttnParams p) {
 #pragma unroll
     for (int n = 0; n < DPL; ++n) acc[nt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  wave_attend<HD, NT, false>(p, sv, qf, lim, 0, t_stop, 32, m_run, l_run, acc);
+  wave_attend<HD, NT, false, kPrefillDepth>(p, sv, qf, lim, 0, t_stop, 32, m_run, l_run, acc);
 
   // acc[nt][n][r] = O[row li + 16nt][d = DPL*(4lq + r) + n]: the lane owns 4*DPL consecutive
   // head-dim elements of its row, starting at 4*DPL*lq.
@@ -537,9 +776,14 @@ static size_t ws_floats_o(int batch, int R, int n_kv, int head_dim, int64_t max_
   return size_t(batch) * n_kv * size_t(max_splits) * R * head_dim;
 }
 
+// Workspace layout: a fixed counter region of kMaxCounters int32 (so that no call's partials
+// ever land where another call's counters live) | partial O | (m, l) pairs.
+constexpr int kMaxCounters = 16384;
+constexpr size_t kCounterBytes = size_t(kMaxCounters) * 4;
+
 static size_t ws_bytes(int batch, int R, int n_kv, int head_dim, int64_t max_splits) {
   const size_t rows = size_t(batch) * n_kv * size_t(max_splits) * R;
-  return (ws_floats_o(batch, R, n_kv, head_dim, max_splits) + rows * 2) * sizeof(float);
+  return kCounterBytes + (ws_floats_o(batch, R, n_kv, head_dim, max_splits) + rows * 2) * sizeof(float);
 }
 
 static int validate_attn(const char* fn, const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, const void* k_new,
@@ -590,7 +834,9 @@ static void fill_params(AttnParams& p, const void* q, int64_t q_sb, int64_t q_ss
   p.o_sb = o_sb; p.o_ss = o_ss; p.o_sh = o_sh;
   p.ws_o = nullptr;
   p.ws_ml = nullptr;
+  p.ws_cnt = nullptr;
   p.status = status;
+  p.batch = 0;
   p.s_q = s_q;
   p.g = n_heads / n_kv;
   p.R = s_q * p.g;
@@ -602,17 +848,16 @@ static void fill_params(AttnParams& p, const void* q, int64_t q_sb, int64_t q_ss
   p.max_splits = 1;
   p.causal = causal ? 1 : 0;
   p.has_new = k_new ? 1 : 0;
+  p.two_pass = 0;
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
 }
 
 template <int HD, int NT, int W>
 static void launch_decode_t(const AttnParams& p, int batch, hipStream_t stream) {
-  dim3 grid(p.max_splits, p.n_kv, batch);
-  decode_kernel<HD, NT, W><<<grid, 64 * W, 0, stream>>>(p);
-  if (p.max_splits > 1) {
-    dim3 cgrid((p.R * (HD / 8) + 255) / 256, p.n_kv, batch);
-    combine_kernel<HD><<<cgrid, 256, 0, stream>>>(p);
-  }
+  // upper bound of the dense item count; items past the real total exit at once
+  const int64_t items = int64_t(batch) * p.n_kv * p.max_splits;
+  decode_kernel<HD, NT, W><<<dim3(unsigned(items)), 64 * W, 0, stream>>>(p);
+  if (p.two_pass && p.max_splits > 1) combine_kernel<HD><<<dim3(1, p.n_kv, batch), 256, 0, stream>>>(p);
 }
 
 template <int HD>
@@ -656,7 +901,8 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
                                int64_t o_sb, int64_t o_ss, int64_t o_sh, void* workspace, size_t workspace_bytes,
                                int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv, int32_t head_dim,
                                int32_t page_size, int32_t num_pages, int32_t max_blocks, int32_t causal,
-                               float softmax_scale, int32_t split_tokens, int32_t* status, void* stream) {
+                               float softmax_scale, int32_t split_tokens, int32_t flags, int32_t* status,
+                               void* stream) {
   using namespace pkv;
   clear_error();
   const char* fn = "pkv_decode_attn";
@@ -678,12 +924,20 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
               page_size, num_pages, max_blocks, causal, softmax_scale, status);
   p.split_tokens = st;
   p.max_splits = int(ms);
+  p.batch = batch;
+  if (int64_t(batch) * n_kv * ms > (int64_t(1) << 30))
+    return fail(PKV_EINVAL, "%s: %lld work items exceed the grid limit", fn, (long long)(int64_t(batch) * n_kv * ms));
+  p.two_pass = (flags & PKV_DECODE_TWO_PASS) ? 1 : 0;
   if (ms > 1) {
     const size_t need = ws_bytes(batch, R, n_kv, head_dim, ms);
     if (!workspace || workspace_bytes < need)
       return fail(PKV_ENOSPC, "%s: workspace %zu bytes < %zu needed", fn, workspace_bytes, need);
     if (!aligned16(workspace)) return fail(PKV_EINVAL, "%s: workspace not 16-byte aligned", fn);
-    p.ws_o = static_cast<float*>(workspace);
+    if (int64_t(batch) * n_kv > kMaxCounters)
+      return fail(PKV_EINVAL, "%s: batch * n_kv = %lld exceeds %d split-K counters; pass split_tokens >= "
+                  "max_blocks * page_size", fn, (long long)batch * n_kv, kMaxCounters);
+    p.ws_cnt = static_cast<int32_t*>(workspace);
+    p.ws_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
     p.ws_ml = p.ws_o + ws_floats_o(batch, R, n_kv, head_dim, ms);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -717,6 +971,12 @@ extern "C" int pkv_prefill_attn(const void* q, int64_t q_sb, int64_t q_ss, int64
               cache_page_stride, block_table, bt_stride, cache_seqlens, out, o_sb, o_ss, o_sh, s_q, n_heads, n_kv,
               page_size, num_pages, max_blocks, causal, softmax_scale, status);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (k_new) {
+    rc = launch_append(fn, k_new, kn_sb, kn_ss, kn_sh, v_new, vn_sb, vn_ss, vn_sh, k_cache, v_cache,
+                       cache_page_stride, block_table, bt_stride, cache_seqlens, batch, s_q, n_kv, head_dim,
+                       page_size, num_pages, max_blocks, status, s);
+    if (rc) return rc;
+  }
   if (head_dim == 128)
     launch_prefill_hd<128>(p, batch, s);
   else

@@ -15,11 +15,12 @@ pytestmark = pytest.mark.gpu
 
 
 def _run_and_check(gpu, *, batch, ctx, page_size, n_kv, n_heads, head_dim, s_q, causal=True, append=True,
-                   split_tokens=0, seed=0, kernel="auto", extra_cols=0, what=""):
+                   split_tokens=0, seed=0, kernel="auto", extra_cols=0, two_pass=False, what=""):
     cpu, dev = make_paged_case(gpu, batch=batch, ctx=ctx, page_size=page_size, n_kv=n_kv, n_heads=n_heads,
                                head_dim=head_dim, s_q=s_q, seed=seed, extra_cols=extra_cols)
     print(f"case {what} B={batch} ctx={list(ctx)[:6]} P={page_size} kv={n_kv} h={n_heads} hd={head_dim} "
-          f"s_q={s_q} causal={causal} append={append} split={split_tokens} kernel={kernel}", flush=True)
+          f"s_q={s_q} causal={causal} append={append} split={split_tokens} kernel={kernel} two_pass={two_pass}",
+          flush=True)
     kw = dict(cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"], causal=causal)
     k = dev["k"] if append else None
     v = dev["v"] if append else None
@@ -27,7 +28,7 @@ def _run_and_check(gpu, *, batch, ctx, page_size, n_kv, n_heads, head_dim, s_q, 
         out = prism_amd.prefill_attention(dev["q"], dev["k_cache"], dev["v_cache"], k, v, **kw)
     else:
         out = prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], k, v,
-                                                split_tokens=split_tokens, **kw)
+                                                split_tokens=split_tokens, two_pass=two_pass, **kw)
     torch.cuda.synchronize()
     ref, kb, vb = pa.flash_attn_with_kvcache_ref(
         cpu["q"], cpu["k_cache"], cpu["v_cache"], cpu["k"] if append else None, cpu["v"] if append else None,
@@ -62,6 +63,16 @@ def test_decode_append_attention(gpu, case):
 def test_decode_split_invariance(gpu, split):
     _run_and_check(gpu, batch=3, ctx=[1500, 33, 700], page_size=256, n_kv=4, n_heads=28, head_dim=128, s_q=1,
                    split_tokens=split, what=f"split{split}")
+
+
+def test_split_merge_rearms_across_calls_and_matches_two_pass(gpu):
+    # consecutive calls of different shapes share one workspace: the in-kernel merge counters
+    # must be back at zero after every call, and the two-pass merge must agree
+    shapes = [(2, [5000, 40]), (6, [3000, 17, 4100, 800, 1, 2500]), (3, [9000, 600, 1]), (1, [33])]
+    for i, (B, ctx) in enumerate(shapes * 2):
+        for two_pass in (False, True):
+            _run_and_check(gpu, batch=B, ctx=ctx, page_size=256, n_kv=4, n_heads=28, head_dim=128, s_q=1,
+                           split_tokens=256, seed=i, two_pass=two_pass, what=f"rearm{i}")
 
 
 def test_decode_without_append_and_non_causal(gpu):
