@@ -8,9 +8,10 @@ attention over it (prism_amd.flash_attn_with_kvcache, the drop-in for Prism's pe
 engine/executor.py:260-261).  Inputs are resident in HBM before timing; every layer reads its own
 cache, so a step streams the whole working set and the 256 MB Infinity Cache cannot serve it.
 
-Prints one JSON line: value = algorithmic HBM bytes per step / step time (GB/s), plus the per-call
-roofline (HIP events around every attention call on the stream it runs on) and a CPU baseline (the
-oracle's torch-CPU reference path on a bounded sample of the same workload, rank 0, N=1 only).
+The step is captured once in a HIP graph and replayed (as Prism's executor runs decode); HIP events
+on the replay stream bracket the K timed replays.  Prints one JSON line: value = algorithmic HBM
+bytes per step / step time (GB/s), the per-call roofline (step time / 28 calls) and a CPU baseline
+(the oracle's torch-CPU reference path on a bounded sample of the same workload, N=1 only).
 """
 from __future__ import annotations
 
@@ -36,6 +37,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = library choice)")
     ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--merge", choices=["auto", "two-pass", "fused"], default="auto",
+                    help="split-K merge: library choice, second launch, or inside the attention launch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=4, help="layers in the CPU baseline sample")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -104,7 +107,6 @@ def main() -> int:
               "path (the paged KV hot path shards by KV head / sequence; see DESIGN.md). Use --gpus 1.",
               file=sys.stderr)
         return 2
-    import numpy as np
     import torch
 
     import prism_amd
@@ -121,33 +123,43 @@ def main() -> int:
     def call(l):
         prism_amd.flash_attn_with_kvcache(w.q[l], kv.k_caches[l], kv.v_caches[l], k=w.k[l], v=w.v[l],
                                           cache_seqlens=w.cache_seqlens, block_table=w.block_table,
-                                          causal=True, out=outs[l], split_tokens=args.split)
+                                          causal=True, out=outs[l], split_tokens=args.split,
+                                          two_pass={"auto": None, "two-pass": True, "fused": False}[args.merge])
 
-    for _ in range(args.warmup):
+    def step():
         for l in range(L):
             call(l)
-    torch.cuda.synchronize()
-    print(f"[bench] warmup done ({args.warmup} steps)", file=sys.stderr, flush=True)
 
+    # An eager step sizes the split-K workspace; the step is then captured in a HIP graph and
+    # replayed, as Prism's executor runs decode (engine/executor.py:272-310, :358-360).
+    step()
+    torch.cuda.synchronize()
+    cap = torch.cuda.Stream(device=dev)
+    cap.wait_stream(torch.cuda.current_stream(dev))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cap):
+        step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=cap):
+            step()
+    torch.cuda.current_stream(dev).wait_stream(cap)
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    print(f"[bench] warmup done ({args.warmup} graph replays)", file=sys.stderr, flush=True)
+
+    # HIP events on the replay stream bracket exactly the K timed steps.
     stream = torch.cuda.current_stream(dev)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(args.steps * L)]
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record(stream)
-    i = 0
     for _ in range(args.steps):
-        for l in range(L):
-            ev[i][0].record(stream)
-            call(l)
-            ev[i][1].record(stream)
-            i += 1
+        graph.replay()
     t_end.record(stream)
     torch.cuda.synchronize()
     step_ms = t_start.elapsed_time(t_end) / args.steps
-    call_us = [a.elapsed_time(b) * 1e3 for a, b in ev]
-    avg_call_us = float(np.mean(call_us))
+    avg_call_us = step_ms * 1e3 / L
     status = prism_amd.read_status(dev)
     if status:
         print(f"[bench] WARNING: kernel status flags {status}", file=sys.stderr)
@@ -156,8 +168,8 @@ def main() -> int:
     bytes_step = bytes_layer * L
     value = bytes_step / (step_ms * 1e-3) / 1e9
     achieved = bytes_layer / (avg_call_us * 1e-6) / 1e9
-    print(f"[bench] step {step_ms * 1e3:.1f} us, call avg {avg_call_us:.2f} us "
-          f"(min {min(call_us):.2f}, max {max(call_us):.2f}), {achieved:.0f} GB/s", file=sys.stderr, flush=True)
+    print(f"[bench] step {step_ms * 1e3:.1f} us, call avg {avg_call_us:.2f} us, {achieved:.0f} GB/s",
+          file=sys.stderr, flush=True)
 
     if args.copy_probe_mib:
         n_pages = max(1, args.copy_probe_mib * (1 << 20) // (kv.bytes_per_page * 2 * L))
@@ -190,7 +202,7 @@ def main() -> int:
             "batch": w.batch, "layers": L, "n_heads": w.n_heads, "n_kv": kv.num_kv_heads,
             "head_dim": kv.head_dim, "page_size": kv.page_size, "pool_pages": kv.max_pages,
             "sum_ctx": int(w.ctx.sum()), "max_ctx": int(w.ctx.max()), "seed": args.seed,
-            "split_tokens": args.split or "auto",
+            "split_tokens": args.split or "auto", "merge": args.merge,
         },
         "roofline": {
             "bound": "hbm",
@@ -199,7 +211,9 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "flash_attn_with_kvcache call (decode_kernel + split-K combine), HIP events",
+            "kernel": "decode_rows_kernel (append + paged attention over whole 1 KiB token rows, "
+                      "split-K partials) + combine_kernel<128> (split-K merge); HIP events around K graph "
+                      "replays of the 28-call step, per call = step / 28",
             "bytes_per_call": bytes_layer,
             "avg_call_us": round(avg_call_us, 3),
         },

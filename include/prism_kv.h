@@ -46,8 +46,9 @@ extern "C" {
 
 #define PKV_STATUS_BAD_PAGE 1
 
-/* pkv_decode_attn flags */
-#define PKV_DECODE_TWO_PASS 1 /* merge split-K partials in a second launch instead of in-kernel */
+/* pkv_decode_attn flags (neither = the library picks the faster merge for the kernel it runs) */
+#define PKV_DECODE_TWO_PASS 1    /* merge split-K partials in a second launch */
+#define PKV_DECODE_FUSED_MERGE 2 /* merge them in the attention launch (last workgroup to finish) */
 
 /* ABI version of the loaded library (PKV_ABI_VERSION it was built with). */
 int pkv_abi_version(void);
@@ -92,9 +93,10 @@ size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, i
  * 1/sqrt(head_dim)); softmax and accumulation are fp32, out is bf16 [batch, s_q, n_heads,
  * head_dim] with the given strides.  A query row with no visible key gets zeros.
  * split_tokens (multiple of 32, or 0 = library choice) is the KV range one workgroup reduces
- * before the split-K merge.  By default the last workgroup of a (sequence, KV head) to finish
- * merges the partials inside the same launch; flags = PKV_DECODE_TWO_PASS merges them in a
- * second launch instead (same results up to fp32 rounding order).  workspace must hold pkv_decode_workspace_bytes() bytes and be
+ * before the split-K merge.  flags = PKV_DECODE_TWO_PASS merges the partials in a second
+ * launch; PKV_DECODE_FUSED_MERGE lets the last workgroup of a sequence to finish merge them
+ * inside the attention launch; 0 picks per kernel (results agree up to fp32 rounding order).
+ * workspace must hold pkv_decode_workspace_bytes() bytes and be
  * zero-filled before its first use; every call leaves it in that state again (its first 64 KiB
  * hold per-(sequence, KV head) arrival counters, so batch * n_kv <= 16384 when a sequence can
  * span more than one split).  Calls that share a workspace must be ordered (same

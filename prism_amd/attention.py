@@ -82,6 +82,12 @@ def _workspace(device: torch.device, nbytes: int, stream: int) -> torch.Tensor |
         return ws
 
 
+def _merge_flags(two_pass: bool | None) -> int:
+    if two_pass is None:
+        return 0
+    return _lib.PKV_DECODE_TWO_PASS if two_pass else _lib.PKV_DECODE_FUSED_MERGE
+
+
 def _rows(t: torch.Tensor, name: str, nheads: int, hd: int) -> tuple[int, int, int]:
     if t.dtype != _BF16:
         raise RuntimeError(f"{name} must be bfloat16, got {t.dtype}")
@@ -163,7 +169,7 @@ def flash_attn_with_kvcache(
     *,
     out: torch.Tensor | None = None,
     split_tokens: int = 0,
-    two_pass: bool = False,
+    two_pass: bool | None = None,
     status: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Append k/v into the paged cache and attend (see module docstring for the contract).
@@ -171,7 +177,8 @@ def flash_attn_with_kvcache(
     Arguments Prism never passes (rotary_*, cache_batch_idx, cache_leftpad, window_size,
     softcap, alibi_slopes, return_softmax_lse) must keep their defaults.  ``num_splits`` > 0
     fixes the number of KV splits per sequence; ``split_tokens`` > 0 (a multiple of 32) fixes
-    the split length directly; ``two_pass`` merges split-K partials in a second launch.
+    the split length directly; ``two_pass`` True merges split-K partials in a second launch, False
+    inside the attention launch, None lets the library pick for the kernel it runs.
     """
     if rotary_cos is not None or rotary_sin is not None or cache_batch_idx is not None \
             or cache_leftpad is not None or tuple(window_size) != (-1, -1) or softcap != 0.0 \
@@ -243,7 +250,7 @@ def flash_attn_with_kvcache(
             out.data_ptr(), *os_,
             ws.data_ptr() if ws is not None else 0, ws.numel() if ws is not None else 0,
             batch, s_q, n_heads, n_kv, hd, page_size, num_pages, max_blocks,
-            1 if causal else 0, scale, int(split_tokens), _lib.PKV_DECODE_TWO_PASS if two_pass else 0,
+            1 if causal else 0, scale, int(split_tokens), _merge_flags(two_pass),
             st.data_ptr(), stream)
         _lib.check(rc, "pkv_decode_attn")
     else:
@@ -259,7 +266,7 @@ def flash_attn_with_kvcache(
 
 
 def decode_attention(q, k_cache, v_cache, k=None, v=None, *, cache_seqlens, block_table,
-                     causal=True, softmax_scale=None, split_tokens=0, two_pass=False, out=None, status=None):
+                     causal=True, softmax_scale=None, split_tokens=0, two_pass=None, out=None, status=None):
     """Force the split-K decode kernel (s_q * n_heads / n_kv <= 64)."""
     n_kv = k_cache.shape[2]
     if q.shape[1] * (q.shape[2] // n_kv) > 64:

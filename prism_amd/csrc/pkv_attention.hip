@@ -502,7 +502,7 @@ __device__ __forceinline__ float ld_coherent(const float* ptr) {
 // Log-sum-exp merge of the n_split partials of (b, h) into the bf16 output, by `nthreads` threads.
 // Splits are merged kMergeChunk at a time with every load of a chunk issued before any is used,
 // so the merge costs one memory round trip per chunk rather than one per split.
-constexpr int kMergeChunk = 4;
+constexpr int kMergeChunk = 8;
 
 template <int HD>
 __device__ __forceinline__ void combine_splits(const AttnParams& p, int b, int h, int n_split, int tid, int nthreads) {
@@ -553,6 +553,9 @@ __device__ __forceinline__ void combine_splits(const AttnParams& p, int b, int h
 // (b, h) arrival counter; the last split to arrive merges all partials and writes the output, and
 // resets the counter to zero for the next call.  One launch per call, no separate combine pass.
 // ---------------------------------------------------------------------------------------------
+#ifndef PKV_DECODE_W
+#define PKV_DECODE_W 4
+#endif
 #ifndef PKV_DECODE_MIN_BLOCKS
 #define PKV_DECODE_MIN_BLOCKS 1
 #endif
@@ -674,16 +677,326 @@ __global__ __launch_bounds__(64 * W, PKV_DECODE_MIN_BLOCKS) void decode_kernel(c
   if (threadIdx.x == 0) __hip_atomic_store(p.ws_cnt + (b * p.n_kv + h), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Two-pass mode: the split-K merge as its own launch (kernel boundaries order everything).
+// Two-pass mode: the split-K merge as its own launch.  The kernel boundary orders the partial
+// stores before these loads, so plain vector loads serve, and every split's loads of a thread are
+// issued before any is used: one memory round trip per kMergeBatch splits.  Grid (n_kv, batch);
+// thread t of the workgroup owns (row, 4 head-dim elements) = (t / (HD/4), t % (HD/4)).
+constexpr int kMergeBatch = 32;
+
 template <int HD>
-__global__ __launch_bounds__(256) void combine_kernel(const AttnParams p) {
-  const int h = blockIdx.y;
-  const int b = blockIdx.z;
+__global__ __launch_bounds__(512) void combine_kernel(const AttnParams p) {
+  constexpr int Q4 = HD / 4;
+  __shared__ float sm_m_in[kMergeBatch][16], sm_l_in[kMergeBatch][16];
+  __shared__ float sm_m[16], sm_l[16], sm_rescale[16];
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
   int c, L;
   seq_lengths(p, b, c, L);
-  const int n_split_b = num_splits(p, L);
-  if (n_split_b <= 1) return;
-  combine_splits<HD>(p, b, h, n_split_b, threadIdx.x, 256);
+  const int n_split = num_splits(p, L);
+  if (n_split <= 1) return;
+  const int row = threadIdx.x / Q4;
+  const int d0 = (threadIdx.x - row * Q4) * 4;
+  const bool active = row < p.R;
+  const int64_t base = int64_t(b * p.n_kv + h) * p.max_splits * p.R;
+  if (threadIdx.x < 16) {
+    sm_m[threadIdx.x] = -INFINITY;
+    sm_l[threadIdx.x] = 0.f;
+  }
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < n_split; s0 += kMergeBatch) {
+    const int ns = min(kMergeBatch, n_split - s0);
+    f32x4 x[kMergeBatch];
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u)
+      x[u] = (active && u < ns) ? *reinterpret_cast<const f32x4*>(p.ws_o + (base + int64_t(s0 + u) * p.R + row) * HD + d0)
+                                : f32x4{0.f, 0.f, 0.f, 0.f};
+    // (m, l) of every (split, row) of the batch into LDS, one pair per thread
+    {
+      const int u = threadIdx.x / 16, r = threadIdx.x % 16;
+      const bool ok = u < ns && r < p.R;
+      const f32x2 ml = ok ? *reinterpret_cast<const f32x2*>(p.ws_ml + (base + int64_t(s0 + u) * p.R + r) * 2)
+                          : f32x2{-INFINITY, 0.f};
+      sm_m_in[u][r] = ml[0];
+      sm_l_in[u][r] = ml[1];
+    }
+    __syncthreads();
+    if (threadIdx.x < 16) {
+      const int r = threadIdx.x;
+      float M = sm_m[r];
+      for (int u = 0; u < ns; ++u) M = fmaxf(M, sm_m_in[u][r]);
+      const float M_use = (M == -INFINITY) ? 0.f : M;
+      const float rescale = fast_exp2(sm_m[r] - M_use);
+      float lsum = sm_l[r] * rescale;
+      for (int u = 0; u < ns; ++u) {
+        const float w = fast_exp2(sm_m_in[u][r] - M_use);
+        lsum += w * sm_l_in[u][r];
+        sm_m_in[u][r] = w;  // now the batch weight
+      }
+      sm_m[r] = M;
+      sm_l[r] = lsum;
+      sm_rescale[r] = rescale;
+    }
+    __syncthreads();
+    if (active) {
+      o *= sm_rescale[row];
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u)
+        if (u < ns) o += sm_m_in[u][row] * x[u];
+    }
+    __syncthreads();  // the batch's weights are consumed before the next batch overwrites them
+  }
+  if (active) {
+    const float inv = sm_l[row] > 0.f ? 1.f / sm_l[row] : 0.f;
+    const int j = row / p.g;
+    const int hq = row - j * p.g;
+    const u32x2 ov = {pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv)};
+    *reinterpret_cast<u32x2*>(p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + d0) = ov;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Row-streaming decode for the shape the 7B decode step runs at (head_dim 128, 4 KV heads,
+// pages of >= 32 rows, <= 16 query rows per KV head).
+//
+// Reading one KV head's 256-byte slice out of every 1 KiB token row (what decode_kernel does, one
+// workgroup per head) opens each DRAM row four times, at different moments, from four
+// workgroups; whole rows stream ~30% faster.  Here a workgroup owns a (sequence, split) for all
+// four heads.  Each 32-token tile of K and of V is one contiguous 32 KiB run of its page; the
+// workgroup copies it into LDS with global_load_lds_dwordx4 (no VGPR staging, tracked by vmcnt),
+// double-buffered so tile i+1 streams in while tile i is consumed, and wave h then reads head
+// h's MFMA operands from LDS.  The 16-byte chunks of row r are XOR-swizzled by
+// g(r) = (r & 3) | ((r >> 3) & 3) << 2, so every group of 8 or 16 consecutive lanes hits distinct
+// bank groups both for the K-operand reads (16 rows, one chunk) and the V-operand reads (one row,
+// 16 chunks).  Workgroups are persistent (one per CU, the 128 KiB of LDS allows
+// no more) and walk the dense (sequence, split) items with a grid stride; each wave's softmax
+// state is per head, so no cross-wave merge is needed, and splits of a sequence are merged by
+// the last of its workgroups to finish, through the same coherent-store protocol as
+// decode_kernel, with one arrival counter per sequence.
+// ---------------------------------------------------------------------------------------------
+namespace rows {
+// chunk swizzle of row r (bits 0-3 of the 16-byte chunk index; stays inside the head's 256 B)
+__device__ __forceinline__ int swz(int r) { return (r & 3) | (((r >> 3) & 3) << 2); }
+constexpr int HD = 128;
+constexpr int NKV = 4;
+constexpr int ROW_BYTES = NKV * HD * 2;   // 1 KiB
+constexpr int TILE = 32;                  // tokens per tile
+constexpr int TILE_BYTES = TILE * ROW_BYTES;
+typedef __attribute__((address_space(3))) void lds_void;
+}  // namespace rows
+
+// Workgroup barrier that only orders memory operations for the compiler: the hardware waits for
+// nothing beyond the explicit s_waitcnt the caller issued (a __syncthreads fence would also
+// drain the next tile's in-flight LDS copies, serialising the double buffer).
+__device__ __forceinline__ void raw_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ void rows_wait_vm(bool keep_one_tile) {
+  // vmcnt <= 16 (the next tile's copies may stay in flight) or vmcnt == 0
+  if (keep_one_tile)
+    __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16): [3:0] = 0, [15:14] = 1; expcnt/lgkmcnt: no wait
+  else
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+}
+
+// Copy tile rows of K and V at token T0 (all heads) into LDS buffer `buf` (K then V); each wave
+// copies rows wave, wave + 4, ... with lane l writing LDS chunk l of the row from global chunk
+// l ^ swz(row).
+__device__ __forceinline__ void rows_issue_tile(const AttnParams& p, const SeqView& sv, int T0, BtWindow& btw,
+                                                char* buf) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  // the window loaded at the item's first page covers the whole item (split <= 32 pages)
+  const int pid = __builtin_amdgcn_readlane(btw.ids, (T0 >> p.log2_page) - btw.col0);
+  const bool ok = unsigned(pid) < unsigned(p.num_pages);
+  if (!ok && T0 < sv.t_end) flag_status(p.status, PKV_STATUS_BAD_PAGE);
+  const int64_t off = int64_t(ok ? pid : 0) * p.page_stride + int64_t(T0 & ((1 << p.log2_page) - 1)) * (rows::NKV * rows::HD);
+  const char* kg = uniform_ptr(reinterpret_cast<const char*>(p.k_cache + off));
+  const char* vg = uniform_ptr(reinterpret_cast<const char*>(p.v_cache + off));
+#pragma unroll
+  for (int i = 0; i < rows::TILE / rows::NKV; ++i) {
+    const int r = i * rows::NKV + wave;
+    const uint32_t src = uint32_t(r * rows::ROW_BYTES + ((lane ^ rows::swz(r)) << 4));
+    __builtin_amdgcn_global_load_lds(kg + src, (rows::lds_void*)(buf + r * rows::ROW_BYTES), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(vg + src, (rows::lds_void*)(buf + rows::TILE_BYTES + r * rows::ROW_BYTES), 16, 0, 0);
+  }
+}
+
+// Head-h MFMA operands of the tile in LDS buffer `buf` into registers (same layout as load_tile).
+__device__ __forceinline__ void rows_read_tile(const char* buf, int h, int T0, int t_end, KVTile<128>& tl) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15;
+  const int lq = lane >> 4;
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+    const int r = 8 * (li >> 2) + 4 * a + (li & 3);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int chunk = h * 16 + ((4 * kk + lq) ^ rows::swz(r));
+      tl.kr[a][kk] = *reinterpret_cast<const u32x4*>(buf + r * rows::ROW_BYTES + chunk * 16);
+    }
+  }
+  const char* vb = buf + rows::TILE_BYTES;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int r = 8 * lq + e;
+    const int chunk = h * 16 + (li ^ rows::swz(r));
+    const u32x4 v = *reinterpret_cast<const u32x4*>(vb + r * rows::ROW_BYTES + chunk * 16);
+    const bool keep = T0 + r < t_end;  // rows past the sequence: P = 0 must not meet a stale NaN
+    tl.vr[e].w[0] = keep ? v[0] : 0u;
+    tl.vr[e].w[1] = keep ? v[1] : 0u;
+    tl.vr[e].w[2] = keep ? v[2] : 0u;
+    tl.vr[e].w[3] = keep ? v[3] : 0u;
+  }
+}
+
+// Append the new rows of every head that fall in tokens [a0, a1) of sequence sv.b.
+__device__ __forceinline__ void rows_append(const AttnParams& p, const SeqView& sv, int a0, int a1) {
+  constexpr int CPR = rows::HD / 8;
+  const int per_row = rows::NKV * CPR * 2;
+  const int n_items = (a1 - a0) * per_row;
+  for (int idx = threadIdx.x; idx < n_items; idx += 64 * rows::NKV) {
+    const int row = idx / per_row;
+    int rem = idx - row * per_row;
+    const bool is_v = rem >= rows::NKV * CPR;
+    if (is_v) rem -= rows::NKV * CPR;
+    const int hh = rem / CPR;
+    const int c8 = rem - hh * CPR;
+    const int t = a0 + row;
+    const int j = t - sv.c;
+    const int col = t >> p.log2_page;
+    const int pid = col < p.max_blocks ? sv.bt[col] : -1;
+    if (pid < 0 || pid >= p.num_pages) {
+      flag_status(p.status, PKV_STATUS_BAD_PAGE);
+      continue;
+    }
+    const int64_t dst = int64_t(pid) * p.page_stride + int64_t(t & ((1 << p.log2_page) - 1)) * (rows::NKV * rows::HD) +
+                        hh * rows::HD + c8 * 8;
+    const uint16_t* src = is_v ? p.v_new + sv.b * p.vn_sb + j * p.vn_ss + hh * p.vn_sh
+                               : p.k_new + sv.b * p.kn_sb + j * p.kn_ss + hh * p.kn_sh;
+    st16((is_v ? p.v_cache : p.k_cache) + dst, ld16(src + c8 * 8));
+  }
+}
+
+__global__ __launch_bounds__(256, 1) void decode_rows_kernel(const AttnParams p) {
+  constexpr int HD = rows::HD;
+  constexpr int DPL = HD / 16;
+  __shared__ __attribute__((aligned(16))) char lds[2][2 * rows::TILE_BYTES];
+  __shared__ int sm_last;
+
+  const int lane = threadIdx.x & 63;
+  const int h = threadIdx.x >> 6;  // one wave per KV head
+  const int li = lane & 15;
+  const int lq = lane >> 4;
+
+  for (int item = blockIdx.x;; item += gridDim.x) {
+    int b, split;
+    if (!locate_item(p, p.batch, item, b, split)) break;
+    int c, L;
+    seq_lengths(p, b, c, L);
+    const int t_begin = split * p.split_tokens;
+    const int n_split_b = num_splits(p, L);
+    SeqView sv;
+    sv.b = b;
+    sv.h = h;
+    sv.c = c;
+    sv.t_end = min(t_begin + p.split_tokens, L);
+    sv.bt = p.block_table + int64_t(b) * p.bt_stride;
+
+    if (p.has_new) {
+      rows_append(p, sv, max(max(c, t_begin), 0), sv.t_end);
+      __syncthreads();
+    }
+
+    bf16x8 qf[1][HD / 32];
+    int lim[1];
+    load_q<HD, 1>(p, sv, L, 0, qf, lim);
+    float m_run[1] = {-INFINITY}, l_run[1] = {0.f};
+    f32x4 acc[1][DPL];
+#pragma unroll
+    for (int n = 0; n < DPL; ++n) acc[0][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    int lim_min = lim[0] < 0 ? 0x7fffffff : lim[0];
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) lim_min = min(lim_min, __shfl_xor(lim_min, off, 64));
+    lim_min = __builtin_amdgcn_readfirstlane(lim_min);
+
+    const int n_tiles = (sv.t_end - t_begin + rows::TILE - 1) / rows::TILE;
+    BtWindow btw;
+    bt_window_load(p, sv, t_begin >> p.log2_page, btw);
+    if (n_tiles > 0) rows_issue_tile(p, sv, t_begin, btw, lds[0]);
+    if (n_tiles > 1) rows_issue_tile(p, sv, t_begin + rows::TILE, btw, lds[1]);
+    // Q and the block-table window (issued before the tile copies) have landed once at most the
+    // two tiles' 32 copies are outstanding; saying so here keeps the loop entry from waiting for
+    // the tile copies too.
+    __builtin_amdgcn_s_waitcnt(0x8F70);  // vmcnt(32)
+    for (int i = 0; i < n_tiles; ++i) {
+      const int T0 = t_begin + i * rows::TILE;
+      rows_wait_vm(i + 1 < n_tiles);  // this wave's copies of tile i have landed
+      raw_barrier();                  // ... and every other wave's
+      KVTile<HD> tl;
+      rows_read_tile(lds[i & 1], h, T0, sv.t_end, tl);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
+      raw_barrier();                       // nobody reads buffer i & 1 any more
+      if (i + 2 < n_tiles) rows_issue_tile(p, sv, T0 + 2 * rows::TILE, btw, lds[i & 1]);
+      compute_tile<HD, 1, true>(p, tl, T0, qf, lim, lim_min, m_run, l_run, acc);
+    }
+
+    // ---- epilogue: wave h owns head h's rows li < R ----
+    const float lsum = sum_over_quads(l_run[0]);
+    if (n_split_b == 1) {
+      if (li < p.R) {
+        const int j = li / p.g;
+        const int hq = li - j * p.g;
+        const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+        uint16_t* dst = p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + 4 * DPL * lq;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          u32x4 ov;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[0][2 * k][r] * inv, acc[0][2 * k + 1][r] * inv);
+          st16(dst + DPL * r, ov);
+        }
+      }
+      continue;
+    }
+    if (li < p.R) {
+      const int64_t slot = (int64_t(b * p.n_kv + h) * p.max_splits + split) * p.R + li;
+      float* dst = p.ws_o + slot * HD + 4 * DPL * lq;
+      if (p.two_pass) {
+        // read back by a later launch: plain vector stores, the kernel boundary orders them
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          *reinterpret_cast<f32x4*>(dst + DPL * r) = f32x4{acc[0][0][r], acc[0][1][r], acc[0][2][r], acc[0][3][r]};
+          *reinterpret_cast<f32x4*>(dst + DPL * r + 4) = f32x4{acc[0][4][r], acc[0][5][r], acc[0][6][r], acc[0][7][r]};
+        }
+        if (lq == 0) *reinterpret_cast<f32x2*>(p.ws_ml + slot * 2) = f32x2{m_run[0], lsum};
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int n = 0; n < DPL; ++n) st_coherent(dst + DPL * r + n, acc[0][n][r]);
+        if (lq == 0) {
+          st_coherent(p.ws_ml + slot * 2, m_run[0]);
+          st_coherent(p.ws_ml + slot * 2 + 1, lsum);
+        }
+      }
+    }
+    if (p.two_pass) continue;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int prev = atomicAdd(p.ws_cnt + b, 1);
+      sm_last = (prev == n_split_b - 1);
+    }
+    __syncthreads();
+    if (sm_last) {
+      combine_splits<HD>(p, b, h, n_split_b, lane, 64);
+      __syncthreads();
+      if (threadIdx.x == 0) __hip_atomic_store(p.ws_cnt + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -764,7 +1077,33 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(const AttnParams p) {
 // ---------------------------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------------------------
-static int choose_split_tokens(int split_tokens) { return split_tokens > 0 ? split_tokens : 512; }
+// Default KV range per workgroup: the row-streaming kernel (one persistent workgroup per CU)
+// wants enough items to balance its grid stride; decode_kernel wants fewer, longer items.
+constexpr int kRowsSplitDefault = 256;
+constexpr int kHeadSplitDefault = 512;
+
+static bool use_rows_kernel(int head_dim, int n_kv, int R, int page_size, int split_tokens, int32_t flags) {
+  (void)flags;
+  return head_dim == rows::HD && n_kv == rows::NKV && R <= 16 && page_size >= 32 &&
+         (split_tokens <= 0 || split_tokens <= 32 * page_size);
+}
+
+static int choose_split_tokens(int split_tokens, bool rows_path = false) {
+  if (split_tokens > 0) return split_tokens;
+  return rows_path ? kRowsSplitDefault : kHeadSplitDefault;
+}
+
+static int device_cu_count() {
+  static int counts[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (counts[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    counts[dev] = n;
+  }
+  return counts[dev];
+}
 
 static int64_t max_splits_for(int split_tokens, int page_size, int max_blocks) {
   const int64_t cap = int64_t(max_blocks) * page_size;
@@ -857,13 +1196,13 @@ static void launch_decode_t(const AttnParams& p, int batch, hipStream_t stream) 
   // upper bound of the dense item count; items past the real total exit at once
   const int64_t items = int64_t(batch) * p.n_kv * p.max_splits;
   decode_kernel<HD, NT, W><<<dim3(unsigned(items)), 64 * W, 0, stream>>>(p);
-  if (p.two_pass && p.max_splits > 1) combine_kernel<HD><<<dim3(1, p.n_kv, batch), 256, 0, stream>>>(p);
+  if (p.two_pass && p.max_splits > 1) combine_kernel<HD><<<dim3(p.n_kv, batch), 512, 0, stream>>>(p);
 }
 
 template <int HD>
 static void launch_decode_hd(const AttnParams& p, int batch, hipStream_t stream) {
   switch ((p.R + 15) / 16) {
-    case 1: launch_decode_t<HD, 1, 4>(p, batch, stream); break;
+    case 1: launch_decode_t<HD, 1, PKV_DECODE_W>(p, batch, stream); break;
     case 2: launch_decode_t<HD, 2, 4>(p, batch, stream); break;
     case 3: launch_decode_t<HD, 3, 2>(p, batch, stream); break;
     default: launch_decode_t<HD, 4, 2>(p, batch, stream); break;
@@ -888,7 +1227,8 @@ extern "C" size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t
   using namespace pkv;
   if (batch <= 0 || s_q <= 0 || n_kv <= 0 || n_heads <= 0 || max_blocks <= 0 || page_size <= 0 || head_dim <= 0)
     return 0;
-  const int st = choose_split_tokens(split_tokens);
+  // the default split differs between the two decode kernels: size for the smaller one
+  const int st = split_tokens > 0 ? split_tokens : min(kRowsSplitDefault, kHeadSplitDefault);
   const int64_t ms = max_splits_for(st, page_size, max_blocks);
   if (ms <= 1) return 0;
   return ws_bytes(batch, s_q * (n_heads / n_kv), n_kv, head_dim, ms);
@@ -912,7 +1252,11 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
   if (rc) return rc;
   const int R = s_q * (n_heads / n_kv);
   if (R > 64) return fail(PKV_EINVAL, "%s: s_q * n_heads / n_kv = %d > 64; use pkv_prefill_attn", fn, R);
-  const int st = choose_split_tokens(split_tokens);
+  if ((flags & ~(PKV_DECODE_TWO_PASS | PKV_DECODE_FUSED_MERGE)) ||
+      (flags & (PKV_DECODE_TWO_PASS | PKV_DECODE_FUSED_MERGE)) == (PKV_DECODE_TWO_PASS | PKV_DECODE_FUSED_MERGE))
+    return fail(PKV_EINVAL, "%s: bad flags 0x%x", fn, unsigned(flags));
+  const bool rows_path = use_rows_kernel(head_dim, n_kv, R, page_size, split_tokens, flags);
+  const int st = choose_split_tokens(split_tokens, rows_path);
   if (st % 32) return fail(PKV_EINVAL, "%s: split_tokens %d must be a positive multiple of 32", fn, st);
   const int64_t ms = max_splits_for(st, page_size, max_blocks);
   if (ms > 65535) return fail(PKV_EINVAL, "%s: %lld splits exceed the grid limit", fn, (long long)ms);
@@ -927,7 +1271,9 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
   p.batch = batch;
   if (int64_t(batch) * n_kv * ms > (int64_t(1) << 30))
     return fail(PKV_EINVAL, "%s: %lld work items exceed the grid limit", fn, (long long)(int64_t(batch) * n_kv * ms));
-  p.two_pass = (flags & PKV_DECODE_TWO_PASS) ? 1 : 0;
+  // The row-streaming kernel saturates HBM up to its last tile, so its partials are best merged
+  // by a second launch; the head-parallel kernel merges in place (no second launch).
+  p.two_pass = (flags & PKV_DECODE_TWO_PASS) ? 1 : (flags & PKV_DECODE_FUSED_MERGE) ? 0 : rows_path ? 1 : 0;
   if (ms > 1) {
     const size_t need = ws_bytes(batch, R, n_kv, head_dim, ms);
     if (!workspace || workspace_bytes < need)
@@ -941,10 +1287,16 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
     p.ws_ml = p.ws_o + ws_floats_o(batch, R, n_kv, head_dim, ms);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (head_dim == 128)
+  if (rows_path) {
+    const int64_t items = int64_t(batch) * ms;
+    const int grid = int(items < device_cu_count() ? items : device_cu_count());
+    decode_rows_kernel<<<grid, 64 * rows::NKV, 0, s>>>(p);
+    if (p.two_pass && p.max_splits > 1) combine_kernel<128><<<dim3(p.n_kv, batch), 512, 0, s>>>(p);
+  } else if (head_dim == 128) {
     launch_decode_hd<128>(p, batch, s);
-  else
+  } else {
     launch_decode_hd<64>(p, batch, s);
+  }
   return check_launch(fn);
 }
 
