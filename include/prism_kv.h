@@ -46,9 +46,11 @@ extern "C" {
 
 #define PKV_STATUS_BAD_PAGE 1
 
-/* pkv_decode_attn flags (neither = the library picks the faster merge for the kernel it runs) */
-#define PKV_DECODE_TWO_PASS 1    /* merge split-K partials in a second launch */
-#define PKV_DECODE_FUSED_MERGE 2 /* merge them in the attention launch (last workgroup to finish) */
+/* pkv_decode_attn flags (0 = the library's choice of kernel and merge) */
+#define PKV_DECODE_TWO_PASS 1    /* per-head kernel: merge split-K partials in a second launch */
+#define PKV_DECODE_FUSED_MERGE 2 /* per-head kernel, partials merged by the last workgroup to finish */
+#define PKV_DECODE_HEADS 4       /* use the per-head kernel where the balanced one would run */
+#define PKV_DECODE_GRID(n) ((int32_t)(n) << 8) /* balanced kernel on n (1..65535) workgroups, not one per CU */
 
 /* ABI version of the loaded library (PKV_ABI_VERSION it was built with). */
 int pkv_abi_version(void);
@@ -74,7 +76,8 @@ int pkv_append(const void* k_new, int64_t kn_sb, int64_t kn_ss, int64_t kn_sh,
 /*
  * Bytes of workspace pkv_decode_attn needs for these sizes (split-K partial outputs and
  * log-sum-exp terms).  split_tokens = 0 asks for the library's own choice, exactly as
- * pkv_decode_attn would make it.
+ * pkv_decode_attn would make it with flags = 0 (a PKV_DECODE_GRID(n) above the device's CU count
+ * needs 65536 + 2 n * 4 * R * 130 * 4 bytes, R = s_q * n_heads / n_kv).
  */
 size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv,
                                   int32_t head_dim, int32_t page_size, int32_t max_blocks,
@@ -92,10 +95,13 @@ size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, i
  * h / (n_heads / n_kv).  Scores are scaled by softmax_scale (Prism uses the default
  * 1/sqrt(head_dim)); softmax and accumulation are fp32, out is bf16 [batch, s_q, n_heads,
  * head_dim] with the given strides.  A query row with no visible key gets zeros.
- * split_tokens (multiple of 32, or 0 = library choice) is the KV range one workgroup reduces
- * before the split-K merge.  flags = PKV_DECODE_TWO_PASS merges the partials in a second
- * launch; PKV_DECODE_FUSED_MERGE lets the last workgroup of a sequence to finish merge them
- * inside the attention launch; 0 picks per kernel (results agree up to fp32 rounding order).
+ * Two kernels serve the call.  Where head_dim = 128, n_kv = 4, page_size >= 32,
+ * s_q * n_heads / n_kv <= 16 and batch <= 256 (the Qwen2.5-7B decode shape), split_tokens = 0 and
+ * neither PKV_DECODE_HEADS nor PKV_DECODE_FUSED_MERGE is set, a balanced kernel gives every
+ * workgroup an equal share of all sequences' 32-token KV tiles and a second launch merges the
+ * sequences that straddle shares.  Otherwise a per-(sequence, KV head, split) kernel reduces
+ * split_tokens keys (a multiple of 32; 0 = 512) per workgroup and merges the splits inside the
+ * launch (PKV_DECODE_TWO_PASS: in a second launch).  Results agree up to fp32 rounding order.
  * workspace must hold pkv_decode_workspace_bytes() bytes and be
  * zero-filled before its first use; every call leaves it in that state again (its first 64 KiB
  * hold per-(sequence, KV head) arrival counters, so batch * n_kv <= 16384 when a sequence can

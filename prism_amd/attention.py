@@ -82,10 +82,17 @@ def _workspace(device: torch.device, nbytes: int, stream: int) -> torch.Tensor |
         return ws
 
 
-def _merge_flags(two_pass: bool | None) -> int:
-    if two_pass is None:
-        return 0
-    return _lib.PKV_DECODE_TWO_PASS if two_pass else _lib.PKV_DECODE_FUSED_MERGE
+def _decode_flags(two_pass: bool | None, kernel: str, grid: int) -> int:
+    flags = 0
+    if two_pass is not None:
+        flags |= _lib.PKV_DECODE_TWO_PASS if two_pass else _lib.PKV_DECODE_FUSED_MERGE
+    if kernel == "heads":
+        flags |= _lib.PKV_DECODE_HEADS
+    elif kernel != "auto":
+        raise ValueError(f"kernel must be 'auto' or 'heads', got {kernel!r}")
+    if not 0 <= int(grid) <= 0xFFFF:
+        raise ValueError(f"grid {grid} outside [0, 65535]")
+    return flags | (int(grid) << 8)
 
 
 def _rows(t: torch.Tensor, name: str, nheads: int, hd: int) -> tuple[int, int, int]:
@@ -170,6 +177,8 @@ def flash_attn_with_kvcache(
     out: torch.Tensor | None = None,
     split_tokens: int = 0,
     two_pass: bool | None = None,
+    kernel: str = "auto",
+    grid: int = 0,
     status: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Append k/v into the paged cache and attend (see module docstring for the contract).
@@ -177,8 +186,10 @@ def flash_attn_with_kvcache(
     Arguments Prism never passes (rotary_*, cache_batch_idx, cache_leftpad, window_size,
     softcap, alibi_slopes, return_softmax_lse) must keep their defaults.  ``num_splits`` > 0
     fixes the number of KV splits per sequence; ``split_tokens`` > 0 (a multiple of 32) fixes
-    the split length directly; ``two_pass`` True merges split-K partials in a second launch, False
-    inside the attention launch, None lets the library pick for the kernel it runs.
+    the split length directly (both select the per-head kernel); ``two_pass`` True merges that
+    kernel's split-K partials in a second launch, False inside the attention launch, None lets the
+    library choose.  ``kernel="heads"`` forces the per-head kernel where the balanced one would
+    run; ``grid`` > 0 runs the balanced kernel on that many workgroups instead of one per CU.
     """
     if rotary_cos is not None or rotary_sin is not None or cache_batch_idx is not None \
             or cache_leftpad is not None or tuple(window_size) != (-1, -1) or softcap != 0.0 \
@@ -250,7 +261,7 @@ def flash_attn_with_kvcache(
             out.data_ptr(), *os_,
             ws.data_ptr() if ws is not None else 0, ws.numel() if ws is not None else 0,
             batch, s_q, n_heads, n_kv, hd, page_size, num_pages, max_blocks,
-            1 if causal else 0, scale, int(split_tokens), _merge_flags(two_pass),
+            1 if causal else 0, scale, int(split_tokens), _decode_flags(two_pass, kernel, grid),
             st.data_ptr(), stream)
         _lib.check(rc, "pkv_decode_attn")
     else:
@@ -266,14 +277,16 @@ def flash_attn_with_kvcache(
 
 
 def decode_attention(q, k_cache, v_cache, k=None, v=None, *, cache_seqlens, block_table,
-                     causal=True, softmax_scale=None, split_tokens=0, two_pass=None, out=None, status=None):
+                     causal=True, softmax_scale=None, split_tokens=0, two_pass=None, kernel="auto", grid=0,
+                     out=None, status=None):
     """Force the split-K decode kernel (s_q * n_heads / n_kv <= 64)."""
     n_kv = k_cache.shape[2]
     if q.shape[1] * (q.shape[2] // n_kv) > 64:
         raise RuntimeError("decode_attention needs s_q * n_heads / n_kv <= 64")
     return flash_attn_with_kvcache(q, k_cache, v_cache, k, v, cache_seqlens=cache_seqlens,
                                    block_table=block_table, causal=causal, softmax_scale=softmax_scale,
-                                   split_tokens=split_tokens, two_pass=two_pass, out=out, status=status)
+                                   split_tokens=split_tokens, two_pass=two_pass, kernel=kernel, grid=grid,
+                                   out=out, status=status)
 
 
 def prefill_attention(q, k_cache, v_cache, k=None, v=None, *, cache_seqlens, block_table,

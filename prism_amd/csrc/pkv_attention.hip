@@ -48,6 +48,7 @@ struct AttnParams {
   int32_t* status;
   int batch, s_q, g, R, n_kv, log2_page, num_pages, max_blocks, split_tokens, max_splits;
   int causal, has_new, two_pass;
+  int lean_grid;  // workgroups of a decode_lean_kernel launch (its combine needs the same split)
   float scale_log2;  // softmax_scale * log2(e)
 };
 
@@ -755,23 +756,35 @@ __global__ __launch_bounds__(512) void combine_kernel(const AttnParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Row-streaming decode for the shape the 7B decode step runs at (head_dim 128, 4 KV heads,
-// pages of >= 32 rows, <= 16 query rows per KV head).
+// Balanced row-streaming decode for the shape the 7B decode step runs at (head_dim 128, 4 KV
+// heads, pages of >= 32 rows, <= 16 query rows per KV head, <= 256 sequences).
 //
-// Reading one KV head's 256-byte slice out of every 1 KiB token row (what decode_kernel does, one
+// Reading one KV head's 256-byte slice out of every 1 KiB token row (decode_kernel, one
 // workgroup per head) opens each DRAM row four times, at different moments, from four
-// workgroups; whole rows stream ~30% faster.  Here a workgroup owns a (sequence, split) for all
-// four heads.  Each 32-token tile of K and of V is one contiguous 32 KiB run of its page; the
-// workgroup copies it into LDS with global_load_lds_dwordx4 (no VGPR staging, tracked by vmcnt),
-// double-buffered so tile i+1 streams in while tile i is consumed, and wave h then reads head
-// h's MFMA operands from LDS.  The 16-byte chunks of row r are XOR-swizzled by
-// g(r) = (r & 3) | ((r >> 3) & 3) << 2, so every group of 8 or 16 consecutive lanes hits distinct
-// bank groups both for the K-operand reads (16 rows, one chunk) and the V-operand reads (one row,
-// 16 chunks).  Workgroups are persistent (one per CU, the 128 KiB of LDS allows
-// no more) and walk the dense (sequence, split) items with a grid stride; each wave's softmax
-// state is per head, so no cross-wave merge is needed, and splits of a sequence are merged by
-// the last of its workgroups to finish, through the same coherent-store protocol as
-// decode_kernel, with one arrival counter per sequence.
+// workgroups; whole rows stream ~30% faster.  Here one workgroup handles all four heads of the
+// tokens it owns (wave h = KV head h).
+//
+// Work split.  Every sequence is cut into 32-token tiles (a sequence without keys still counts
+// one tile, which yields its zero output); the tiles of all sequences, in sequence order, form
+// one list of T tiles, and persistent workgroup w of G owns the contiguous range
+// [w * per, (w + 1) * per), per = ceil(T / G).  Every workgroup streams the same bytes to within
+// one tile, whatever the context lengths.  The sequences a range touches are its segments; a
+// segment holding a whole sequence writes the bf16 output directly, the others (at most the
+// first and the last segment of a range) write an fp32 partial (m, l, O) to workspace slot
+// 2w (first segment of the range) or 2w + 1 (last), merged by combine_lean_kernel.
+//
+// Streaming.  A 32-token tile of K and of V is one contiguous 32 KiB run of its page, copied
+// into LDS with global_load_lds_dwordx4 (no VGPR staging, tracked by vmcnt) and double-buffered
+// so tile j+1 streams in while tile j is consumed; wave h then reads head h's MFMA operands from
+// LDS.  The 16-byte chunks of row r are XOR-swizzled by g(r) = (r & 3) | ((r >> 3) & 3) << 2, so
+// every group of 8 or 16 consecutive lanes hits distinct bank groups both for the K-operand
+// reads (16 rows, one chunk) and the V-operand reads (one row, 16 chunks).  A segment's Q
+// operand and a tile's new rows are loaded along with the tile copies, two tiles ahead.
+//
+// Append.  The tile holding a sequence's new rows is copied from the cache like any other (its
+// new rows are stale there); each wave then overwrites its head's slice of those rows in LDS
+// from registers and stores the same bytes to the cache.  Only this workgroup touches those
+// rows during the launch, so nothing orders the append before the attention reads.
 // ---------------------------------------------------------------------------------------------
 namespace rows {
 // chunk swizzle of row r (bits 0-3 of the 16-byte chunk index; stays inside the head's 256 B)
@@ -781,6 +794,14 @@ constexpr int NKV = 4;
 constexpr int ROW_BYTES = NKV * HD * 2;   // 1 KiB
 constexpr int TILE = 32;                  // tokens per tile
 constexpr int TILE_BYTES = TILE * ROW_BYTES;
+constexpr int kMaxBatch = 256;            // sequences the in-register scan covers
+constexpr int kChunks = kMaxBatch / 64;
+constexpr int Q_BYTES = 16 * NKV * HD * 2; // Q operand area: <= 16 rows x 4 heads x 256 B
+constexpr int BUF_BYTES = 2 * TILE_BYTES + Q_BYTES;  // one LDS buffer: K tile | V tile | Q
+// Cache policy of the K/V tile copies: non-temporal (the nt bit).  Every cache byte is read once
+// per call, and streaming it past the caches' normal allocation measured ~12% faster for the
+// 7B decode step's 115 MB (18.7 vs 21.1 us per launch for the bare copy loop).
+constexpr int kStreamPolicy = 2;
 typedef __attribute__((address_space(3))) void lds_void;
 }  // namespace rows
 
@@ -801,26 +822,181 @@ __device__ __forceinline__ void rows_wait_vm(bool keep_one_tile) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 }
 
-// Copy tile rows of K and V at token T0 (all heads) into LDS buffer `buf` (K then V); each wave
-// copies rows wave, wave + 4, ... with lane l writing LDS chunk l of the row from global chunk
-// l ^ swz(row).
-__device__ __forceinline__ void rows_issue_tile(const AttnParams& p, const SeqView& sv, int T0, BtWindow& btw,
-                                                char* buf) {
+// Inclusive prefix sum over the 64 lanes: shifts inside each 16-lane row, then the GFX9 row
+// broadcasts carry the row totals on (lane 15 into row 1 and lane 47 into row 3, then lane 31
+// into rows 2 and 3).  A lane whose source falls outside its row adds 0.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return v;
+}
+
+__device__ __forceinline__ int tiles_of(int L) { return L > 0 ? (L + rows::TILE - 1) / rows::TILE : 1; }
+
+// Every sequence's clamped lengths and first tile, 64 sequences per register (lane l of register
+// q holds sequence 64q + l), from one read of cache_seqlens per wave.  The clamp is seq_lengths'.
+struct SeqTable {
+  int c[rows::kChunks], L[rows::kChunks], first[rows::kChunks];
+  int end[rows::kChunks];  // uniform: one past the last tile of chunk q
+  int total;               // T, tiles over all sequences
+};
+
+__device__ __forceinline__ void seq_table(const AttnParams& p, SeqTable& st) {
+  const int lane = threadIdx.x & 63;
+  const int cap = p.max_blocks << p.log2_page;
+  const int s_new = p.has_new ? p.s_q : 0;
+  int raw[rows::kChunks];
+#pragma unroll
+  for (int q = 0; q < rows::kChunks; ++q) {
+    const int b = 64 * q + lane;
+    raw[q] = 0;
+    if (64 * q < p.batch && b < p.batch) raw[q] = p.seqlens[b];
+  }
+  int base = 0;
+#pragma unroll
+  for (int q = 0; q < rows::kChunks; ++q) {
+    const int b = 64 * q + lane;
+    int c = raw[q];
+    int L = c + s_new;
+    if (b < p.batch && (c < 0 || L > cap)) {
+      if (threadIdx.x < 64) flag_status(p.status, PKV_STATUS_BAD_PAGE);
+      c = min(max(c, 0), cap);
+      L = min(c + s_new, cap);
+    }
+    const int n = b < p.batch ? tiles_of(L) : 0;
+    const int incl = base + wave_incl_scan(n);
+    st.c[q] = c;
+    st.L[q] = L;
+    st.first[q] = incl - n;
+    base = __builtin_amdgcn_readlane(incl, 63);
+    st.end[q] = base;
+  }
+  st.total = base;
+}
+
+// Sequence of tile x (per lane, x < total): its index, first tile and lengths.  A binary search
+// over the chunk's first tiles (non-decreasing across lanes) with lane permutes.
+__device__ __forceinline__ void locate_tile(const AttnParams& p, const SeqTable& st, int x, int& b, int& first,
+                                            int& c, int& L) {
+  b = 0;
+  first = 0;
+  c = 0;
+  L = 0;
+#pragma unroll
+  for (int q = 0; q < rows::kChunks; ++q) {
+    if (64 * q >= p.batch) break;
+    int pos = 0;
+#pragma unroll
+    for (int step = 32; step >= 1; step >>= 1) {
+      const int f = __shfl(st.first[q], min(pos + step, 63), 64);
+      if (pos + step <= 63 && f <= x) pos += step;
+    }
+    const int fq = __shfl(st.first[q], pos, 64);
+    const int cq = __shfl(st.c[q], pos, 64);
+    const int Lq = __shfl(st.L[q], pos, 64);
+    const int lo = q == 0 ? 0 : st.end[q - 1];
+    if (x >= lo && x < st.end[q]) {
+      b = 64 * q + pos;
+      first = fq;
+      c = cq;
+      L = Lq;
+    }
+  }
+}
+
+// Descriptors of tiles x0 + lane (< e) of a workgroup's range: sequence, first token, lengths and
+// page.  A page id outside the pool is flagged (when the tile has keys) and kept as -1.
+struct TileWin {
+  int x0;
+  int b, T0, c, L, pid;
+};
+
+struct TileDesc {
+  int b, T0, c, L, pid;
+};
+
+__device__ __forceinline__ void tile_window(const AttnParams& p, const SeqTable& st, int x0, int e, TileWin& w) {
+  const int lane = threadIdx.x & 63;
+  const int x = min(x0 + lane, e - 1);
+  int b, first, c, L;
+  locate_tile(p, st, x, b, first, c, L);
+  b = min(b, p.batch - 1);
+  const int T0 = (x - first) * rows::TILE;
+  const int col = T0 >> p.log2_page;
+  const int pid = unsigned(col) < unsigned(p.max_blocks) ? p.block_table[int64_t(b) * p.bt_stride + col] : -1;
+  const bool ok = unsigned(pid) < unsigned(p.num_pages);
+  if (!ok && T0 < L && x0 + lane < e && threadIdx.x < 64) flag_status(p.status, PKV_STATUS_BAD_PAGE);
+  w.x0 = x0;
+  w.b = b;
+  w.T0 = T0;
+  w.c = c;
+  w.L = L;
+  w.pid = ok ? pid : -1;
+}
+
+__device__ __forceinline__ TileDesc tile_desc(const TileWin& w, int x) {
+  const int i = x - w.x0;
+  TileDesc d;
+  d.b = __builtin_amdgcn_readlane(w.b, i);
+  d.T0 = __builtin_amdgcn_readlane(w.T0, i);
+  d.c = __builtin_amdgcn_readlane(w.c, i);
+  d.L = __builtin_amdgcn_readlane(w.L, i);
+  d.pid = __builtin_amdgcn_readlane(w.pid, i);
+  return d;
+}
+
+__device__ __forceinline__ bool tile_has_new(const AttnParams& p, const TileDesc& d) {
+  return p.has_new && d.T0 + rows::TILE > d.c && d.T0 < d.L;
+}
+
+// Copies of tile d into LDS buffer `buf`, 16 per wave: K then V rows of every head, wave w taking
+// rows w, w + 4, ..., lane l writing LDS chunk l of a row from global chunk l ^ swz(row).  A row
+// holding one of this call's new tokens (t >= c) is copied from k_new / v_new instead of the
+// cache, so attention sees it without waiting for the append.  When the tile starts a segment
+// (with_q), 4 more copies per wave bring the Q operand rows of head w into the buffer's Q area:
+// row r (clamped to R - 1) at [w][r], LDS chunk l holding global chunk l ^ (r & 15).
+__device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& d, bool with_q, char* buf) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  // the window loaded at the item's first page covers the whole item (split <= 32 pages)
-  const int pid = __builtin_amdgcn_readlane(btw.ids, (T0 >> p.log2_page) - btw.col0);
-  const bool ok = unsigned(pid) < unsigned(p.num_pages);
-  if (!ok && T0 < sv.t_end) flag_status(p.status, PKV_STATUS_BAD_PAGE);
-  const int64_t off = int64_t(ok ? pid : 0) * p.page_stride + int64_t(T0 & ((1 << p.log2_page) - 1)) * (rows::NKV * rows::HD);
+  const int64_t off = int64_t(d.pid < 0 ? 0 : d.pid) * p.page_stride +
+                      int64_t(d.T0 & ((1 << p.log2_page) - 1)) * (rows::NKV * rows::HD);
   const char* kg = uniform_ptr(reinterpret_cast<const char*>(p.k_cache + off));
   const char* vg = uniform_ptr(reinterpret_cast<const char*>(p.v_cache + off));
+  const bool any_new = tile_has_new(p, d);
 #pragma unroll
   for (int i = 0; i < rows::TILE / rows::NKV; ++i) {
     const int r = i * rows::NKV + wave;
-    const uint32_t src = uint32_t(r * rows::ROW_BYTES + ((lane ^ rows::swz(r)) << 4));
-    __builtin_amdgcn_global_load_lds(kg + src, (rows::lds_void*)(buf + r * rows::ROW_BYTES), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(vg + src, (rows::lds_void*)(buf + rows::TILE_BYTES + r * rows::ROW_BYTES), 16, 0, 0);
+    const int t = d.T0 + r;
+    const uint32_t gc = uint32_t(lane ^ rows::swz(r));
+    const char* ks = kg + (r * rows::ROW_BYTES + (gc << 4));
+    const char* vs = vg + (r * rows::ROW_BYTES + (gc << 4));
+    if (any_new && t >= d.c && t < d.L) {
+      const int jn = t - d.c;
+      const int hh = int(gc >> 4);
+      const int w8 = int(gc & 15) * 8;
+      ks = reinterpret_cast<const char*>(p.k_new + d.b * p.kn_sb + jn * p.kn_ss + hh * p.kn_sh + w8);
+      vs = reinterpret_cast<const char*>(p.v_new + d.b * p.vn_sb + jn * p.vn_ss + hh * p.vn_sh + w8);
+    }
+    __builtin_amdgcn_global_load_lds(ks, (rows::lds_void*)(buf + r * rows::ROW_BYTES), 16, 0, rows::kStreamPolicy);
+    __builtin_amdgcn_global_load_lds(vs, (rows::lds_void*)(buf + rows::TILE_BYTES + r * rows::ROW_BYTES), 16, 0,
+                                     rows::kStreamPolicy);
+  }
+  if (with_q) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * i + (lane >> 4);
+      const int rr = min(row, p.R - 1);
+      const int jq = rr / p.g;
+      const int hq = rr - jq * p.g;
+      const int gq = (lane & 15) ^ (row & 15);
+      const uint16_t* src = p.q + d.b * p.q_sb + jq * p.q_ss + (wave * p.g + hq) * p.q_sh + gq * 8;
+      __builtin_amdgcn_global_load_lds(src, (rows::lds_void*)(buf + 2 * rows::TILE_BYTES + (wave * 16 + 4 * i) * 256),
+                                       16, 0, 0);
+    }
   }
 }
 
@@ -852,150 +1028,244 @@ __device__ __forceinline__ void rows_read_tile(const char* buf, int h, int T0, i
   }
 }
 
-// Append the new rows of every head that fall in tokens [a0, a1) of sequence sv.b.
-__device__ __forceinline__ void rows_append(const AttnParams& p, const SeqView& sv, int a0, int a1) {
-  constexpr int CPR = rows::HD / 8;
-  const int per_row = rows::NKV * CPR * 2;
-  const int n_items = (a1 - a0) * per_row;
-  for (int idx = threadIdx.x; idx < n_items; idx += 64 * rows::NKV) {
-    const int row = idx / per_row;
-    int rem = idx - row * per_row;
-    const bool is_v = rem >= rows::NKV * CPR;
-    if (is_v) rem -= rows::NKV * CPR;
-    const int hh = rem / CPR;
-    const int c8 = rem - hh * CPR;
-    const int t = a0 + row;
-    const int j = t - sv.c;
-    const int col = t >> p.log2_page;
-    const int pid = col < p.max_blocks ? sv.bt[col] : -1;
-    if (pid < 0 || pid >= p.num_pages) {
-      flag_status(p.status, PKV_STATUS_BAD_PAGE);
-      continue;
-    }
-    const int64_t dst = int64_t(pid) * p.page_stride + int64_t(t & ((1 << p.log2_page) - 1)) * (rows::NKV * rows::HD) +
-                        hh * rows::HD + c8 * 8;
-    const uint16_t* src = is_v ? p.v_new + sv.b * p.vn_sb + j * p.vn_ss + hh * p.vn_sh
-                               : p.k_new + sv.b * p.kn_sb + j * p.kn_ss + hh * p.kn_sh;
-    st16((is_v ? p.v_cache : p.k_cache) + dst, ld16(src + c8 * 8));
+// Q^T operand (load_q's layout) of head h's rows from the buffer's Q area; rows li >= R get 0.
+__device__ __forceinline__ void rows_read_q(const AttnParams& p, const char* buf, int h, bf16x8 (&qf)[1][4]) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15;
+  const int lq = lane >> 4;
+  const char* qa = buf + 2 * rows::TILE_BYTES + (h * 16 + li) * 256;
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(qa + (((lq + 4 * kk) ^ li) << 4));
+    qf[0][kk] = __builtin_bit_cast(bf16x8, li < p.R ? v : u32x4{0u, 0u, 0u, 0u});
   }
 }
 
-__global__ __launch_bounds__(256, 1) void decode_rows_kernel(const AttnParams p) {
+// Append: store head h's slice of the new rows of tile d, already in LDS buffer `buf`, to the
+// cache (a page id outside the pool was flagged and is skipped).
+__device__ __forceinline__ void rows_append_from_lds(const AttnParams& p, const TileDesc& d, const char* buf) {
+  if (d.pid < 0) return;
+  const int lane = threadIdx.x & 63;
+  const int h = threadIdx.x >> 6;
+  const int li = lane & 15;
+  const int lq = lane >> 4;
+  const int t_lo = max(d.T0, d.c);
+  const int t_hi = min(d.T0 + rows::TILE, d.L);
+  for (int t0 = t_lo; t0 < t_hi; t0 += 4) {
+    const int t = t0 + lq;
+    if (t < t_hi) {
+      const int r = t - d.T0;
+      const int pos = (h * 16 + (li ^ rows::swz(r))) * 16;
+      const u32x4 kv = *reinterpret_cast<const u32x4*>(buf + r * rows::ROW_BYTES + pos);
+      const u32x4 vv = *reinterpret_cast<const u32x4*>(buf + rows::TILE_BYTES + r * rows::ROW_BYTES + pos);
+      const int64_t dst = int64_t(d.pid) * p.page_stride +
+                          int64_t(t & ((1 << p.log2_page) - 1)) * (rows::NKV * rows::HD) + h * rows::HD + 8 * li;
+      st16(p.k_cache + dst, kv);
+      st16(p.v_cache + dst, vv);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p) {
   constexpr int HD = rows::HD;
   constexpr int DPL = HD / 16;
-  __shared__ __attribute__((aligned(16))) char lds[2][2 * rows::TILE_BYTES];
-  __shared__ int sm_last;
+  __shared__ __attribute__((aligned(16))) char lds[2 * rows::BUF_BYTES];
 
   const int lane = threadIdx.x & 63;
   const int h = threadIdx.x >> 6;  // one wave per KV head
   const int li = lane & 15;
   const int lq = lane >> 4;
 
-  for (int item = blockIdx.x;; item += gridDim.x) {
-    int b, split;
-    if (!locate_item(p, p.batch, item, b, split)) break;
-    int c, L;
-    seq_lengths(p, b, c, L);
-    const int t_begin = split * p.split_tokens;
-    const int n_split_b = num_splits(p, L);
-    SeqView sv;
-    sv.b = b;
-    sv.h = h;
-    sv.c = c;
-    sv.t_end = min(t_begin + p.split_tokens, L);
-    sv.bt = p.block_table + int64_t(b) * p.bt_stride;
+  SeqTable st;
+  seq_table(p, st);
+  const int per = (st.total + int(gridDim.x) - 1) / int(gridDim.x);
+  const int s = min(int(blockIdx.x) * per, st.total);
+  const int e = min(s + per, st.total);
+  if (s >= e) return;
+  const int n = e - s;
 
-    if (p.has_new) {
-      rows_append(p, sv, max(max(c, t_begin), 0), sv.t_end);
-      __syncthreads();
-    }
+  TileWin win;
+  tile_window(p, st, s, e, win);
+  TileDesc dA = tile_desc(win, s);
+  TileDesc dB = dA;
+  rows_issue(p, dA, true, lds);
+  if (n > 1) {
+    dB = tile_desc(win, s + 1);
+    rows_issue(p, dB, dB.T0 == 0, lds + rows::BUF_BYTES);
+  }
 
-    bf16x8 qf[1][HD / 32];
-    int lim[1];
-    load_q<HD, 1>(p, sv, L, 0, qf, lim);
-    float m_run[1] = {-INFINITY}, l_run[1] = {0.f};
-    f32x4 acc[1][DPL];
+  bf16x8 qf[1][HD / 32];
+  int lim[1] = {-1};
+  int lim_min = 0x7fffffff;
+  float m_run[1] = {-INFINITY}, l_run[1] = {0.f};
+  f32x4 acc[1][DPL];
 #pragma unroll
-    for (int n = 0; n < DPL; ++n) acc[0][n] = f32x4{0.f, 0.f, 0.f, 0.f};
-    int lim_min = lim[0] < 0 ? 0x7fffffff : lim[0];
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) lim_min = min(lim_min, __shfl_xor(lim_min, off, 64));
-    lim_min = __builtin_amdgcn_readfirstlane(lim_min);
-
-    const int n_tiles = (sv.t_end - t_begin + rows::TILE - 1) / rows::TILE;
-    BtWindow btw;
-    bt_window_load(p, sv, t_begin >> p.log2_page, btw);
-    if (n_tiles > 0) rows_issue_tile(p, sv, t_begin, btw, lds[0]);
-    if (n_tiles > 1) rows_issue_tile(p, sv, t_begin + rows::TILE, btw, lds[1]);
-    // Q and the block-table window (issued before the tile copies) have landed once at most the
-    // two tiles' 32 copies are outstanding; saying so here keeps the loop entry from waiting for
-    // the tile copies too.
-    __builtin_amdgcn_s_waitcnt(0x8F70);  // vmcnt(32)
-    for (int i = 0; i < n_tiles; ++i) {
-      const int T0 = t_begin + i * rows::TILE;
-      rows_wait_vm(i + 1 < n_tiles);  // this wave's copies of tile i have landed
-      raw_barrier();                  // ... and every other wave's
-      KVTile<HD> tl;
-      rows_read_tile(lds[i & 1], h, T0, sv.t_end, tl);
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
-      raw_barrier();                       // nobody reads buffer i & 1 any more
-      if (i + 2 < n_tiles) rows_issue_tile(p, sv, T0 + 2 * rows::TILE, btw, lds[i & 1]);
-      compute_tile<HD, 1, true>(p, tl, T0, qf, lim, lim_min, m_run, l_run, acc);
-    }
-
-    // ---- epilogue: wave h owns head h's rows li < R ----
-    const float lsum = sum_over_quads(l_run[0]);
-    if (n_split_b == 1) {
+  for (int k = 0; k < DPL; ++k) acc[0][k] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int seg_j0 = 0;  // range index of the current segment's first tile
+  int seg_T0 = 0;  // its first token
+  for (int j = 0; j < n; ++j) {
+    const TileDesc d = dA;
+    char* buf = lds + (j & 1) * rows::BUF_BYTES;
+    // This wave's copies of tile j have landed once at most the next tile's group is in flight:
+    // 16 row copies, plus 4 Q copies when that tile starts a segment (stores issued later only
+    // make the wait stricter).
+    if (j + 1 >= n)
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    else if (dB.T0 == 0)
+      __builtin_amdgcn_s_waitcnt(0x4F74);  // vmcnt(20)
+    else
+      __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16)
+    raw_barrier();                         // ... and every other wave's
+    if (j == 0 || d.T0 == 0) {
+      // a segment starts: its Q operand, row limits and a fresh softmax state
+      rows_read_q(p, buf, h, qf);
+      seg_j0 = j;
+      seg_T0 = d.T0;
+      lim[0] = -1;
       if (li < p.R) {
-        const int j = li / p.g;
-        const int hq = li - j * p.g;
-        const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-        uint16_t* dst = p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + 4 * DPL * lq;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          u32x4 ov;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[0][2 * k][r] * inv, acc[0][2 * k + 1][r] * inv);
-          st16(dst + DPL * r, ov);
-        }
+        const int jr = li / p.g;
+        const int last = p.causal ? (d.L - p.s_q + jr) : (d.L - 1);
+        lim[0] = min(last, d.L - 1);
       }
-      continue;
+      lim_min = lim[0] < 0 ? 0x7fffffff : lim[0];
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) lim_min = min(lim_min, __shfl_xor(lim_min, off, 64));
+      lim_min = __builtin_amdgcn_readfirstlane(lim_min);
+      m_run[0] = -INFINITY;
+      l_run[0] = 0.f;
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) acc[0][k] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    if (li < p.R) {
-      const int64_t slot = (int64_t(b * p.n_kv + h) * p.max_splits + split) * p.R + li;
-      float* dst = p.ws_o + slot * HD + 4 * DPL * lq;
-      if (p.two_pass) {
-        // read back by a later launch: plain vector stores, the kernel boundary orders them
+    if (tile_has_new(p, d)) rows_append_from_lds(p, d, buf);
+    KVTile<HD> tl;
+    rows_read_tile(buf, h, d.T0, d.L, tl);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
+    raw_barrier();                       // nobody reads this buffer any more
+    if (j + 2 < n) {
+      const int x2 = s + j + 2;
+      if (x2 - win.x0 >= 64) tile_window(p, st, x2, e, win);
+      const TileDesc d2 = tile_desc(win, x2);
+      rows_issue(p, d2, d2.T0 == 0, buf);
+      dA = dB;
+      dB = d2;
+    } else {
+      dA = dB;
+    }
+    if (d.T0 < d.L) compute_tile<HD, 1, true>(p, tl, d.T0, qf, lim, lim_min, m_run, l_run, acc);
+
+    if (j + 1 < n && d.T0 + rows::TILE < d.L) continue;  // the segment goes on
+    // ---- segment epilogue: wave h owns head h's rows li < R ----
+    const float lsum = sum_over_quads(l_run[0]);
+    if (li >= p.R) {
+      // padding rows: nothing to write
+    } else if (seg_T0 == 0 && d.T0 + rows::TILE >= d.L) {
+      // the whole sequence: final output
+      const int jr = li / p.g;
+      const int hq = li - jr * p.g;
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      uint16_t* dst = p.out + d.b * p.o_sb + jr * p.o_ss + (h * p.g + hq) * p.o_sh + 4 * DPL * lq;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          *reinterpret_cast<f32x4*>(dst + DPL * r) = f32x4{acc[0][0][r], acc[0][1][r], acc[0][2][r], acc[0][3][r]};
-          *reinterpret_cast<f32x4*>(dst + DPL * r + 4) = f32x4{acc[0][4][r], acc[0][5][r], acc[0][6][r], acc[0][7][r]};
-        }
-        if (lq == 0) *reinterpret_cast<f32x2*>(p.ws_ml + slot * 2) = f32x2{m_run[0], lsum};
-      } else {
+      for (int r = 0; r < 4; ++r) {
+        u32x4 ov;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+        for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[0][2 * k][r] * inv, acc[0][2 * k + 1][r] * inv);
+        st16(dst + DPL * r, ov);
+      }
+    } else {
+      // part of a sequence shared with a neighbouring range: unnormalised partial, merged by the
+      // combine launch (the kernel boundary orders these plain stores before its loads)
+      const int slot = 2 * int(blockIdx.x) + (seg_j0 == 0 ? 0 : 1);
+      const int64_t row = (int64_t(slot) * rows::NKV + h) * p.R + li;
+      float* dst = p.ws_o + row * HD + 4 * DPL * lq;
 #pragma unroll
-          for (int n = 0; n < DPL; ++n) st_coherent(dst + DPL * r + n, acc[0][n][r]);
-        if (lq == 0) {
-          st_coherent(p.ws_ml + slot * 2, m_run[0]);
-          st_coherent(p.ws_ml + slot * 2 + 1, lsum);
-        }
+      for (int r = 0; r < 4; ++r) {
+        *reinterpret_cast<f32x4*>(dst + DPL * r) = f32x4{acc[0][0][r], acc[0][1][r], acc[0][2][r], acc[0][3][r]};
+        *reinterpret_cast<f32x4*>(dst + DPL * r + 4) = f32x4{acc[0][4][r], acc[0][5][r], acc[0][6][r], acc[0][7][r]};
+      }
+      if (lq == 0) *reinterpret_cast<f32x2*>(p.ws_ml + row * 2) = f32x2{m_run[0], lsum};
+    }
+  }
+}
+
+// Merge of the partials a decode_lean_kernel launch of `grid` workgroups left in the workspace:
+// one workgroup per (KV head, sequence); only sequences whose tiles span more than one range
+// have partials.  Thread t owns query row r = t / 32: for the output it owns head-dim elements
+// 4 (t % 32) .. +3, for the weights part t % 32 of the current batch of 32 parts.  Every load of
+// a batch is issued before any is used (one memory round trip per 32 parts).
+__global__ __launch_bounds__(512) void combine_lean_kernel(const AttnParams p, int grid) {
+  constexpr int HD = rows::HD;
+  __shared__ float sm_w[16][33];
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const int r = threadIdx.x >> 5;
+  const int u = threadIdx.x & 31;
+
+  SeqTable st;
+  seq_table(p, st);
+  const int per = (st.total + grid - 1) / grid;
+  int first = 0, L = 0;
+#pragma unroll
+  for (int q = 0; q < rows::kChunks; ++q) {
+    if (q == (b >> 6)) {
+      first = __builtin_amdgcn_readlane(st.first[q], b & 63);
+      L = __builtin_amdgcn_readlane(st.L[q], b & 63);
+    }
+  }
+  const int w0 = first / per;
+  const int w1 = (first + tiles_of(L) - 1) / per;
+  const int np = w1 - w0 + 1;
+  if (np <= 1) return;
+  // the first range holds b in its first segment only if b starts exactly at the range start
+  const int slot0 = 2 * w0 + (first != w0 * per ? 1 : 0);
+  const bool row_ok = r < p.R;
+  float M_run = -INFINITY, l_run = 0.f;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  for (int u0 = 0; u0 < np; u0 += 32) {
+    const int nbat = min(32, np - u0);
+    f32x4 x[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+      x[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (row_ok && k < nbat) {
+        const int part = u0 + k;
+        const int slot = part == 0 ? slot0 : 2 * (w0 + part);
+        x[k] = *reinterpret_cast<const f32x4*>(p.ws_o + ((int64_t(slot) * rows::NKV + h) * p.R + r) * HD + 4 * u);
       }
     }
-    if (p.two_pass) continue;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const int prev = atomicAdd(p.ws_cnt + b, 1);
-      sm_last = (prev == n_split_b - 1);
+    float m = -INFINITY, l = 0.f;
+    if (row_ok && u < nbat) {
+      const int part = u0 + u;
+      const int slot = part == 0 ? slot0 : 2 * (w0 + part);
+      const f32x2 ml = *reinterpret_cast<const f32x2*>(p.ws_ml + ((int64_t(slot) * rows::NKV + h) * p.R + r) * 2);
+      m = ml[0];
+      l = ml[1];
     }
+    float M = m;
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    const float M_new = fmaxf(M_run, M);
+    const float M_use = (M_new == -INFINITY) ? 0.f : M_new;
+    const float w = fast_exp2(m - M_use);
+    float lw = w * l;
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) lw += __shfl_xor(lw, off, 64);
+    const float resc = fast_exp2(M_run - M_use);
+    l_run = l_run * resc + lw;
+    M_run = M_new;
+    sm_w[r][u] = w;
     __syncthreads();
-    if (sm_last) {
-      combine_splits<HD>(p, b, h, n_split_b, lane, 64);
-      __syncthreads();
-      if (threadIdx.x == 0) __hip_atomic_store(p.ws_cnt + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    o *= resc;
+#pragma unroll
+    for (int k = 0; k < 32; ++k)
+      if (k < nbat) o += sm_w[r][k] * x[k];
+    __syncthreads();  // the batch's weights are consumed before the next batch overwrites them
+  }
+  if (row_ok) {
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    const int j = r / p.g;
+    const int hq = r - j * p.g;
+    const u32x2 ov = {pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv)};
+    *reinterpret_cast<u32x2*>(p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + 4 * u) = ov;
   }
 }
 
@@ -1077,21 +1347,8 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(const AttnParams p) {
 // ---------------------------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------------------------
-// Default KV range per workgroup: the row-streaming kernel (one persistent workgroup per CU)
-// wants enough items to balance its grid stride; decode_kernel wants fewer, longer items.
-constexpr int kRowsSplitDefault = 256;
+// Default KV range per workgroup of decode_kernel (decode_lean_kernel splits by range instead).
 constexpr int kHeadSplitDefault = 512;
-
-static bool use_rows_kernel(int head_dim, int n_kv, int R, int page_size, int split_tokens, int32_t flags) {
-  (void)flags;
-  return head_dim == rows::HD && n_kv == rows::NKV && R <= 16 && page_size >= 32 &&
-         (split_tokens <= 0 || split_tokens <= 32 * page_size);
-}
-
-static int choose_split_tokens(int split_tokens, bool rows_path = false) {
-  if (split_tokens > 0) return split_tokens;
-  return rows_path ? kRowsSplitDefault : kHeadSplitDefault;
-}
 
 static int device_cu_count() {
   static int counts[64] = {0};
@@ -1123,6 +1380,26 @@ constexpr size_t kCounterBytes = size_t(kMaxCounters) * 4;
 static size_t ws_bytes(int batch, int R, int n_kv, int head_dim, int64_t max_splits) {
   const size_t rows = size_t(batch) * n_kv * size_t(max_splits) * R;
   return kCounterBytes + (ws_floats_o(batch, R, n_kv, head_dim, max_splits) + rows * 2) * sizeof(float);
+}
+
+// decode_lean_kernel covers the 7B decode shape (head_dim 128, 4 KV heads, pages of >= 32 rows,
+// <= 16 query rows per KV head, <= 256 sequences) and runs there unless the caller fixes
+// split_tokens or asks for decode_kernel (PKV_DECODE_HEADS, PKV_DECODE_FUSED_MERGE).
+static bool use_lean_kernel(int batch, int head_dim, int n_kv, int R, int page_size, int split_tokens,
+                            int32_t flags) {
+  return head_dim == rows::HD && n_kv == rows::NKV && R <= 16 && page_size >= rows::TILE &&
+         batch <= rows::kMaxBatch && split_tokens <= 0 && !(flags & (PKV_DECODE_HEADS | PKV_DECODE_FUSED_MERGE));
+}
+
+// Workgroups of a decode_lean_kernel launch: PKV_DECODE_GRID(n) of the flags, else one per CU.
+static int lean_grid(int32_t flags) {
+  const int g = int((uint32_t(flags) >> 8) & 0xffffu);
+  return g > 0 ? g : device_cu_count();
+}
+
+// Same counter region | partial O [2 grid, n_kv, R, head_dim] | (m, l) [2 grid, n_kv, R, 2].
+static size_t ws_bytes_lean(int grid, int R) {
+  return kCounterBytes + size_t(2) * grid * rows::NKV * R * (rows::HD + 2) * sizeof(float);
 }
 
 static int validate_attn(const char* fn, const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, const void* k_new,
@@ -1188,6 +1465,7 @@ static void fill_params(AttnParams& p, const void* q, int64_t q_sb, int64_t q_ss
   p.causal = causal ? 1 : 0;
   p.has_new = k_new ? 1 : 0;
   p.two_pass = 0;
+  p.lean_grid = 0;
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
 }
 
@@ -1227,11 +1505,16 @@ extern "C" size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t
   using namespace pkv;
   if (batch <= 0 || s_q <= 0 || n_kv <= 0 || n_heads <= 0 || max_blocks <= 0 || page_size <= 0 || head_dim <= 0)
     return 0;
-  // the default split differs between the two decode kernels: size for the smaller one
-  const int st = split_tokens > 0 ? split_tokens : min(kRowsSplitDefault, kHeadSplitDefault);
+  const int R = s_q * (n_heads / n_kv);
+  // enough for either decode kernel the call may run
+  const int st = split_tokens > 0 ? split_tokens : kHeadSplitDefault;
   const int64_t ms = max_splits_for(st, page_size, max_blocks);
-  if (ms <= 1) return 0;
-  return ws_bytes(batch, s_q * (n_heads / n_kv), n_kv, head_dim, ms);
+  size_t need = ms > 1 ? ws_bytes(batch, R, n_kv, head_dim, ms) : 0;
+  if (use_lean_kernel(batch, head_dim, n_kv, R, page_size, split_tokens, 0)) {
+    const size_t lean = ws_bytes_lean(lean_grid(0), R);
+    need = lean > need ? lean : need;
+  }
+  return need;
 }
 
 extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, const void* k_new,
@@ -1252,28 +1535,45 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
   if (rc) return rc;
   const int R = s_q * (n_heads / n_kv);
   if (R > 64) return fail(PKV_EINVAL, "%s: s_q * n_heads / n_kv = %d > 64; use pkv_prefill_attn", fn, R);
-  if ((flags & ~(PKV_DECODE_TWO_PASS | PKV_DECODE_FUSED_MERGE)) ||
-      (flags & (PKV_DECODE_TWO_PASS | PKV_DECODE_FUSED_MERGE)) == (PKV_DECODE_TWO_PASS | PKV_DECODE_FUSED_MERGE))
+  const int32_t merge = flags & (PKV_DECODE_TWO_PASS | PKV_DECODE_FUSED_MERGE);
+  if ((flags & ~(PKV_DECODE_TWO_PASS | PKV_DECODE_FUSED_MERGE | PKV_DECODE_HEADS | PKV_DECODE_GRID(0xffff))) ||
+      merge == (PKV_DECODE_TWO_PASS | PKV_DECODE_FUSED_MERGE))
     return fail(PKV_EINVAL, "%s: bad flags 0x%x", fn, unsigned(flags));
-  const bool rows_path = use_rows_kernel(head_dim, n_kv, R, page_size, split_tokens, flags);
-  const int st = choose_split_tokens(split_tokens, rows_path);
-  if (st % 32) return fail(PKV_EINVAL, "%s: split_tokens %d must be a positive multiple of 32", fn, st);
+  if (split_tokens < 0 || split_tokens % 32)
+    return fail(PKV_EINVAL, "%s: split_tokens %d must be 0 or a positive multiple of 32", fn, split_tokens);
+  const bool lean = use_lean_kernel(batch, head_dim, n_kv, R, page_size, split_tokens, flags);
+  const int st = split_tokens > 0 ? split_tokens : kHeadSplitDefault;
   const int64_t ms = max_splits_for(st, page_size, max_blocks);
   if (ms > 65535) return fail(PKV_EINVAL, "%s: %lld splits exceed the grid limit", fn, (long long)ms);
+  if (int64_t(batch) * n_kv * ms > (int64_t(1) << 30))
+    return fail(PKV_EINVAL, "%s: %lld work items exceed the grid limit", fn, (long long)(int64_t(batch) * n_kv * ms));
   if (batch == 0) return PKV_OK;
 
   AttnParams p;
   fill_params(p, q, q_sb, q_ss, q_sh, k_new, kn_sb, kn_ss, kn_sh, v_new, vn_sb, vn_ss, vn_sh, k_cache, v_cache,
               cache_page_stride, block_table, bt_stride, cache_seqlens, out, o_sb, o_ss, o_sh, s_q, n_heads, n_kv,
               page_size, num_pages, max_blocks, causal, softmax_scale, status);
+  p.batch = batch;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (lean) {
+    // balanced row-streaming kernel; its partials are always merged by a second launch
+    const int grid = lean_grid(flags);
+    const size_t need = ws_bytes_lean(grid, R);
+    if (!workspace || workspace_bytes < need)
+      return fail(PKV_ENOSPC, "%s: workspace %zu bytes < %zu needed", fn, workspace_bytes, need);
+    if (!aligned16(workspace)) return fail(PKV_EINVAL, "%s: workspace not 16-byte aligned", fn);
+    p.ws_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+    p.ws_ml = p.ws_o + size_t(2) * grid * rows::NKV * R * rows::HD;
+    p.two_pass = 1;
+    p.lean_grid = grid;
+    decode_lean_kernel<<<grid, 64 * rows::NKV, 0, s>>>(p);
+    combine_lean_kernel<<<dim3(rows::NKV, batch), 512, 0, s>>>(p, grid);
+    return check_launch(fn);
+  }
+
   p.split_tokens = st;
   p.max_splits = int(ms);
-  p.batch = batch;
-  if (int64_t(batch) * n_kv * ms > (int64_t(1) << 30))
-    return fail(PKV_EINVAL, "%s: %lld work items exceed the grid limit", fn, (long long)(int64_t(batch) * n_kv * ms));
-  // The row-streaming kernel saturates HBM up to its last tile, so its partials are best merged
-  // by a second launch; the head-parallel kernel merges in place (no second launch).
-  p.two_pass = (flags & PKV_DECODE_TWO_PASS) ? 1 : (flags & PKV_DECODE_FUSED_MERGE) ? 0 : rows_path ? 1 : 0;
+  p.two_pass = merge == PKV_DECODE_TWO_PASS ? 1 : 0;
   if (ms > 1) {
     const size_t need = ws_bytes(batch, R, n_kv, head_dim, ms);
     if (!workspace || workspace_bytes < need)
@@ -1286,17 +1586,10 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
     p.ws_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
     p.ws_ml = p.ws_o + ws_floats_o(batch, R, n_kv, head_dim, ms);
   }
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (rows_path) {
-    const int64_t items = int64_t(batch) * ms;
-    const int grid = int(items < device_cu_count() ? items : device_cu_count());
-    decode_rows_kernel<<<grid, 64 * rows::NKV, 0, s>>>(p);
-    if (p.two_pass && p.max_splits > 1) combine_kernel<128><<<dim3(p.n_kv, batch), 512, 0, s>>>(p);
-  } else if (head_dim == 128) {
+  if (head_dim == 128)
     launch_decode_hd<128>(p, batch, s);
-  } else {
+  else
     launch_decode_hd<64>(p, batch, s);
-  }
   return check_launch(fn);
 }
 

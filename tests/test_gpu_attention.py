@@ -15,11 +15,12 @@ pytestmark = pytest.mark.gpu
 
 
 def _run_and_check(gpu, *, batch, ctx, page_size, n_kv, n_heads, head_dim, s_q, causal=True, append=True,
-                   split_tokens=0, seed=0, kernel="auto", extra_cols=0, two_pass=False, what=""):
+                   split_tokens=0, seed=0, kernel="auto", extra_cols=0, two_pass=None, grid=0, what=""):
     cpu, dev = make_paged_case(gpu, batch=batch, ctx=ctx, page_size=page_size, n_kv=n_kv, n_heads=n_heads,
                                head_dim=head_dim, s_q=s_q, seed=seed, extra_cols=extra_cols)
     print(f"case {what} B={batch} ctx={list(ctx)[:6]} P={page_size} kv={n_kv} h={n_heads} hd={head_dim} "
-          f"s_q={s_q} causal={causal} append={append} split={split_tokens} kernel={kernel} two_pass={two_pass}",
+          f"s_q={s_q} causal={causal} append={append} split={split_tokens} kernel={kernel} two_pass={two_pass} "
+          f"grid={grid}",
           flush=True)
     kw = dict(cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"], causal=causal)
     k = dev["k"] if append else None
@@ -28,7 +29,8 @@ def _run_and_check(gpu, *, batch, ctx, page_size, n_kv, n_heads, head_dim, s_q, 
         out = prism_amd.prefill_attention(dev["q"], dev["k_cache"], dev["v_cache"], k, v, **kw)
     else:
         out = prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], k, v,
-                                                split_tokens=split_tokens, two_pass=two_pass, **kw)
+                                                split_tokens=split_tokens, two_pass=two_pass,
+                                                kernel=kernel, grid=grid, **kw)
     torch.cuda.synchronize()
     ref, kb, vb = pa.flash_attn_with_kvcache_ref(
         cpu["q"], cpu["k_cache"], cpu["v_cache"], cpu["k"] if append else None, cpu["v"] if append else None,
@@ -73,6 +75,47 @@ def test_split_merge_rearms_across_calls_and_matches_two_pass(gpu):
         for two_pass in (False, True):
             _run_and_check(gpu, batch=B, ctx=ctx, page_size=256, n_kv=4, n_heads=28, head_dim=128, s_q=1,
                            split_tokens=256, seed=i, two_pass=two_pass, what=f"rearm{i}")
+
+
+# The balanced kernel (head_dim 128, 4 KV heads, pages >= 32, <= 16 query rows per KV head):
+# grids from one workgroup (every tile in one range, several 64-tile descriptor windows) to more
+# workgroups than tiles, ranges holding many short sequences, new rows straddling a tile edge.
+LEAN_CASES = [
+    # (batch, ctx, page, n_heads, s_q, grid, append)
+    (6, [3000, 17, 4100, 800, 1, 2500], 256, 28, 1, 0, True),
+    (6, [3000, 17, 4100, 800, 1, 2500], 256, 28, 1, 1, True),
+    (6, [3000, 17, 4100, 800, 1, 2500], 256, 28, 1, 7, True),
+    (40, [(i * 37) % 300 for i in range(40)], 32, 28, 1, 5, True),
+    (3, [31, 64, 0], 64, 28, 2, 3, True),
+    (2, [61, 700], 256, 16, 4, 4, True),
+    (4, [0, 5, 300, 33], 256, 28, 1, 2, False),
+    (5, [10, 20, 30, 40, 50], 256, 28, 1, 64, True),
+    (70, [(i * 53) % 900 for i in range(70)], 256, 28, 1, 0, True),
+    (70, [(i * 53) % 900 for i in range(70)], 256, 28, 1, 9, True),
+]
+
+
+@pytest.mark.parametrize("case", LEAN_CASES, ids=[f"l{i}" for i in range(len(LEAN_CASES))])
+def test_balanced_decode_kernel(gpu, case):
+    B, ctx, P, nh, s_q, grid, append = case
+    _run_and_check(gpu, batch=B, ctx=ctx, page_size=P, n_kv=4, n_heads=nh, head_dim=128, s_q=s_q,
+                   append=append, grid=grid, seed=len(ctx) + grid, what=f"lean{case[:1] + case[2:]}")
+
+
+@pytest.mark.parametrize("case", [DECODE_CASES[1], DECODE_CASES[4], DECODE_CASES[7]], ids=["d1", "d4", "d7"])
+def test_per_head_kernel_on_balanced_shapes(gpu, case):
+    # the same shapes through the per-(sequence, head, split) kernel, both merges
+    B, ctx, P, n_kv, nh, hd, s_q = case
+    for two_pass in (False, True):
+        _run_and_check(gpu, batch=B, ctx=ctx, page_size=P, n_kv=n_kv, n_heads=nh, head_dim=hd, s_q=s_q,
+                       kernel="heads", two_pass=two_pass, what=f"heads{case}")
+
+
+def test_batch_beyond_balanced_limit(gpu):
+    # more than 256 sequences: the per-head kernel serves the call
+    ctx = [(i * 29) % 200 for i in range(300)]
+    _run_and_check(gpu, batch=300, ctx=ctx, page_size=256, n_kv=4, n_heads=28, head_dim=128, s_q=1,
+                   what="b300")
 
 
 def test_decode_without_append_and_non_causal(gpu):
