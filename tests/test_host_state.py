@@ -1,0 +1,211 @@
+"""Host-side state of the drop-ins where they deliberately differ from the reference (CPU only).
+
+The reference returns every page of a freed sequence to the free list even while a prefix-cache
+entry still points at it (engine/kv_cache.py:87-89), and never shares a page it will write.  The
+product keeps such pages off the free list, shares pages between forked sequences, and copies a
+shared page before the first write into it (copy-on-write).  Page copies are recorded here by a
+CPU stand-in for the kernel launcher; the kernels themselves are checked in test_gpu_pages.py.
+"""
+import numpy as np
+import pytest
+import torch
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+import prism_amd.kv_cache as kvm
+from oracle import page_ops
+from oracle.paged_attention import bf16_bits
+from prism_amd import FlashAttnKVCache, KVCacheOutOfPages, PrefixCache
+
+
+@pytest.fixture
+def copies(monkeypatch):
+    """Replace the page-copy launcher with a CPU copy that records each call."""
+    log = []
+
+    def cpu_copy(src, dst, src_ids, dst_ids, fill):
+        log.append((list(src_ids), list(dst_ids), None if fill is None else list(fill)))
+        for i, (s, d) in enumerate(zip(src_ids, dst_ids)):
+            n = src.page_size if fill is None else fill[i]
+            dst.k_pool[:, d, :n] = src.k_pool[:, s, :n]
+            dst.v_pool[:, d, :n] = src.v_pool[:, s, :n]
+
+    monkeypatch.setattr(kvm, "copy_pages", cpu_copy)
+    return log
+
+
+def _kv(pages=16, P=16, layers=2, seed=0):
+    kv = FlashAttnKVCache(layers, 1, 8, pages, P, "cpu")
+    g = torch.Generator().manual_seed(seed)
+    kv.k_pool.copy_(torch.randn(kv.k_pool.shape, generator=g).to(torch.bfloat16))
+    kv.v_pool.copy_(torch.randn(kv.v_pool.shape, generator=g).to(torch.bfloat16))
+    return kv
+
+
+def _check_invariants(kv):
+    free = kv.free_pages
+    assert len(set(free)) == len(free), "page twice in the free list"
+    held = {p for pages in kv.seq_pages.values() for p in pages}
+    cached = set(kv.prefix_cache.entry_pages()) if kv.prefix_cache is not None else set()
+    assert not (set(free) & held), "live page on the free list"
+    assert not (set(free) & cached), "cached page on the free list"
+    assert set(free) | held | cached == set(range(kv.max_pages)), "page leaked"
+    for p in held:
+        n = sum(pages.count(p) for pages in kv.seq_pages.values())
+        assert kv._holders[p] == n
+    for sid, pages in kv.seq_pages.items():
+        assert len(pages) >= 1 and kv.seq_len[sid] <= len(pages) * kv.page_size
+
+
+def test_out_of_pages_is_both_reference_exception_types():
+    kv = _kv(pages=2)
+    kv.new_sequence(0)
+    kv.new_sequence(1)
+    with pytest.raises(RuntimeError):
+        kv.new_sequence(2)
+    with pytest.raises(IndexError):
+        kv._ensure_capacity(0, 100)
+    assert issubclass(KVCacheOutOfPages, RuntimeError) and issubclass(KVCacheOutOfPages, IndexError)
+
+
+def test_new_sequence_on_a_live_id_frees_its_pages_first():
+    kv = _kv(pages=4)
+    kv.new_sequence(0)
+    kv._ensure_capacity(0, 40)
+    assert kv.pages_used == 3
+    kv.new_sequence(0)
+    assert kv.pages_used == 1 and len(kv.seq_pages[0]) == 1
+    _check_invariants(kv)
+
+
+def test_cached_pages_survive_free_and_return_on_eviction(copies):
+    kv = _kv(pages=8, P=4)
+    pc = PrefixCache(kv, page_size=4)
+    kv.new_sequence(0, "m")
+    kv._ensure_capacity(0, 10)
+    kv.seq_len[0] = 10
+    tokens = list(range(10))
+    pc.store(tokens, kv.seq_pages[0], "m")     # two full blocks cached
+    cached = kv.seq_pages[0][:2]
+    kv.free_sequence(0)
+    assert not set(cached) & set(kv.free_pages)   # the reference would have freed them
+    _check_invariants(kv)
+    # a new request reuses the prefix
+    pages, n = pc.lookup(tokens, "m")
+    assert pages == cached and n == 8
+    kv.new_sequence(1, "m", prefix_pages=pages, prefix_len=n)
+    assert kv.seq_pages[1][:2] == cached and kv.seq_len[1] == 8
+    # evicting while sequence 1 still lists the pages does not free them
+    pc.evict_lru(2)
+    assert not set(cached) & set(kv.free_pages)
+    kv.free_sequence(1)
+    assert set(cached) <= set(kv.free_pages)
+    _check_invariants(kv)
+    assert copies == []
+
+
+def test_fork_and_copy_on_write(copies):
+    kv = _kv(pages=16, P=16)
+    kv.new_sequence(0)
+    kv._ensure_capacity(0, 21)
+    kv.seq_len[0] = 21
+    for sid in (1, 2):
+        kv.fork_sequence(0, sid)
+    shared = list(kv.seq_pages[0])
+    assert kv._holders[shared[1]] == 3 and kv.is_shared(shared[1])
+    before = [bf16_bits(kv.k_pool[l]) for l in range(2)]
+    n = kv.prepare_append([1, 2], 4)
+    assert n == 2 and len(copies) == 1            # one launch for the whole batch
+    src, dst, fill = copies[0]
+    assert src == [shared[1], shared[1]] and fill == [5, 5]
+    assert dst == [kv.seq_pages[1][1], kv.seq_pages[2][1]]
+    assert kv.seq_pages[1][0] == shared[0]        # the full page is not written, stays shared
+    for l in range(2):
+        exp = page_ops.copy_pages([before[l]], [before[l]], src, dst, fill)[0]
+        assert np.array_equal(bf16_bits(kv.k_pool[l]), exp)
+    # parent is now the only holder of page 1: it writes in place
+    assert kv.prepare_append([0], 3) == 0 and kv.seq_pages[0] == shared
+    _check_invariants(kv)
+
+
+def test_write_that_starts_on_a_page_boundary_copies_nothing(copies):
+    kv = _kv(pages=8, P=16)
+    kv.new_sequence(0)
+    kv._ensure_capacity(0, 32)
+    kv.seq_len[0] = 32
+    kv.fork_sequence(0, 1)
+    kv._ensure_capacity(1, 33)                     # new page, no shared page written
+    assert copies == [] and kv.seq_pages[1][:2] == kv.seq_pages[0][:2]
+    _check_invariants(kv)
+
+
+def test_migrate_and_compact_bookkeeping(copies):
+    kv = _kv(pages=12, P=4)
+    pc = PrefixCache(kv, page_size=4)
+    for sid in range(4):
+        kv.new_sequence(sid, owner=f"m{sid % 2}")
+        kv._ensure_capacity(sid, 3 + 4 * sid)
+        kv.seq_len[sid] = 3 + 4 * sid
+    pc.store(list(range(8)), kv.seq_pages[3][:2], "m1")
+    kv.fork_sequence(2, 9)
+    kv.free_sequence(1)
+    live = kv.live_pages()
+    owners = {s: list(p) for s, p in kv.seq_pages.items()}
+    holders = dict(kv._holders)
+    data = {p: kv.k_pool[:, p].clone() for p in live}
+    remap = kv.compact()
+    assert sorted(remap.values()) == list(range(len(live)))
+    assert copies[-1][0] == live and copies[-1][1] == [remap[p] for p in live]
+    for sid, pages in owners.items():
+        assert kv.seq_pages[sid] == [remap[p] for p in pages]
+    assert kv._holders == {remap[p]: n for p, n in holders.items()}
+    for p in live:
+        assert torch.equal(kv.k_pool[:, remap[p]], data[p])
+    assert pc.lookup(list(range(8)), "m1") == ([remap[p] for p in owners[3][:2]], 8)
+    assert kv.pages_used == len(live)
+    _check_invariants(kv)
+
+
+_ops = st.lists(st.tuples(st.sampled_from(["new", "fork", "grow", "free", "store", "evict", "lookup_new"]),
+                          st.integers(0, 7), st.integers(0, 40)), max_size=60)
+
+
+@settings(max_examples=60, deadline=None)
+@given(_ops)
+def test_random_operations_keep_pages_accounted(ops):
+    import prism_amd.kv_cache as m
+
+    saved = m.copy_pages
+    m.copy_pages = lambda src, dst, s, d, f: None     # bookkeeping only
+    try:
+        kv = FlashAttnKVCache(1, 1, 8, 24, 4, "cpu")
+        pc = PrefixCache(kv, page_size=4)
+        for op, a, n in ops:
+            live = sorted(kv.seq_pages)
+            try:
+                if op == "new":
+                    kv.new_sequence(a, "m")
+                elif op == "fork" and live:
+                    kv.fork_sequence(live[a % len(live)], a + 100)
+                elif op == "grow" and live:
+                    sid = live[a % len(live)]
+                    kv.prepare_append([sid], n % 9)
+                    kv.seq_len[sid] += n % 9
+                elif op == "free" and live:
+                    kv.free_sequence(live[a % len(live)])
+                elif op == "store" and live:
+                    sid = live[a % len(live)]
+                    toks = [sid] * kv.seq_len[sid]
+                    pc.store(toks, kv.seq_pages[sid], "m")
+                elif op == "evict":
+                    pc.evict_lru(a % 3)
+                elif op == "lookup_new" and live:
+                    sid = live[a % len(live)]
+                    pages, got = pc.lookup([sid] * kv.seq_len[sid], "m")
+                    if pages:
+                        kv.new_sequence(a + 200, "m", prefix_pages=pages, prefix_len=got)
+            except KVCacheOutOfPages:
+                pass
+            _check_invariants(kv)
+    finally:
+        m.copy_pages = saved
