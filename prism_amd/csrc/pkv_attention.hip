@@ -1187,18 +1187,37 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   }
 }
 
-// Merge of the partials a decode_lean_kernel launch of `grid` workgroups left in the workspace:
-// one workgroup per (KV head, sequence); only sequences whose tiles span more than one range
-// have partials.  Thread t owns query row r = t / 32: for the output it owns head-dim elements
-// 4 (t % 32) .. +3, for the weights part t % 32 of the current batch of 32 parts.  Every load of
-// a batch is issued before any is used (one memory round trip per 32 parts).
-__global__ __launch_bounds__(512) void combine_lean_kernel(const AttnParams p, int grid) {
+// Butterfly max / sum over all 64 lanes without LDS: DPP swaps inside each 16-lane row, then the
+// row swaps of max_over_quads / sum_over_quads.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false)));   // lane ^ 1
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false)));   // lane ^ 2
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false)));  // half-row mirror
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xf, 0xf, false)));  // row mirror
+  return max_over_quads(v);
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xf, 0xf, false));
+  return sum_over_quads(v);
+}
+
+// Merge of the partials a decode_lean_kernel launch of `grid` workgroups left in the workspace.
+// Workgroup (KV head, sequence), one wave per query row; only sequences whose tiles span more than
+// one range have partials.  Lane u holds part u's (m, l) of the row; for the output lane l owns
+// head-dim elements 2l and 2l + 1 and reads them from every part, all loads of a batch of 32
+// parts in flight at once; the parts' weights reach every lane by v_readlane.  No LDS, no barrier.
+constexpr int kLeanMergeBatch = 32;
+
+__global__ __launch_bounds__(1024) void combine_lean_kernel(const AttnParams p, int grid) {
   constexpr int HD = rows::HD;
-  __shared__ float sm_w[16][33];
   const int h = blockIdx.x;
   const int b = blockIdx.y;
-  const int r = threadIdx.x >> 5;
-  const int u = threadIdx.x & 31;
+  const int r = threadIdx.x >> 6;  // query row of this wave
+  const int lane = threadIdx.x & 63;
+  if (r >= p.R) return;
 
   SeqTable st;
   seq_table(p, st);
@@ -1217,56 +1236,42 @@ __global__ __launch_bounds__(512) void combine_lean_kernel(const AttnParams p, i
   if (np <= 1) return;
   // the first range holds b in its first segment only if b starts exactly at the range start
   const int slot0 = 2 * w0 + (first != w0 * per ? 1 : 0);
-  const bool row_ok = r < p.R;
+  auto row_of = [&](int part) {
+    const int slot = part == 0 ? slot0 : 2 * (w0 + part);
+    return (int64_t(slot) * rows::NKV + h) * p.R + r;
+  };
   float M_run = -INFINITY, l_run = 0.f;
-  f32x4 o = {0.f, 0.f, 0.f, 0.f};
-  for (int u0 = 0; u0 < np; u0 += 32) {
-    const int nbat = min(32, np - u0);
-    f32x4 x[32];
+  f32x2 o = {0.f, 0.f};
+  for (int u0 = 0; u0 < np; u0 += kLeanMergeBatch) {
+    const int nb = min(kLeanMergeBatch, np - u0);
+    f32x2 x[kLeanMergeBatch];
 #pragma unroll
-    for (int k = 0; k < 32; ++k) {
-      x[k] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (row_ok && k < nbat) {
-        const int part = u0 + k;
-        const int slot = part == 0 ? slot0 : 2 * (w0 + part);
-        x[k] = *reinterpret_cast<const f32x4*>(p.ws_o + ((int64_t(slot) * rows::NKV + h) * p.R + r) * HD + 4 * u);
-      }
+    for (int k = 0; k < kLeanMergeBatch; ++k) {
+      x[k] = f32x2{0.f, 0.f};
+      if (k < nb) x[k] = *reinterpret_cast<const f32x2*>(p.ws_o + row_of(u0 + k) * HD + 2 * lane);
     }
     float m = -INFINITY, l = 0.f;
-    if (row_ok && u < nbat) {
-      const int part = u0 + u;
-      const int slot = part == 0 ? slot0 : 2 * (w0 + part);
-      const f32x2 ml = *reinterpret_cast<const f32x2*>(p.ws_ml + ((int64_t(slot) * rows::NKV + h) * p.R + r) * 2);
+    if (lane < nb) {
+      const f32x2 ml = *reinterpret_cast<const f32x2*>(p.ws_ml + row_of(u0 + lane) * 2);
       m = ml[0];
       l = ml[1];
     }
-    float M = m;
-#pragma unroll
-    for (int off = 1; off < 32; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-    const float M_new = fmaxf(M_run, M);
+    const float M_new = fmaxf(M_run, wave_max(m));
     const float M_use = (M_new == -INFINITY) ? 0.f : M_new;
     const float w = fast_exp2(m - M_use);
-    float lw = w * l;
-#pragma unroll
-    for (int off = 1; off < 32; off <<= 1) lw += __shfl_xor(lw, off, 64);
     const float resc = fast_exp2(M_run - M_use);
-    l_run = l_run * resc + lw;
+    l_run = l_run * resc + wave_sum(w * l);
     M_run = M_new;
-    sm_w[r][u] = w;
-    __syncthreads();
     o *= resc;
 #pragma unroll
-    for (int k = 0; k < 32; ++k)
-      if (k < nbat) o += sm_w[r][k] * x[k];
-    __syncthreads();  // the batch's weights are consumed before the next batch overwrites them
+    for (int k = 0; k < kLeanMergeBatch; ++k)
+      if (k < nb) o += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), k)) * x[k];
   }
-  if (row_ok) {
-    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-    const int j = r / p.g;
-    const int hq = r - j * p.g;
-    const u32x2 ov = {pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv)};
-    *reinterpret_cast<u32x2*>(p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + 4 * u) = ov;
-  }
+  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+  const int j = r / p.g;
+  const int hq = r - j * p.g;
+  *reinterpret_cast<uint32_t*>(p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + 2 * lane) =
+      pack_bf16x2(o[0] * inv, o[1] * inv);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1567,7 +1572,7 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
     p.two_pass = 1;
     p.lean_grid = grid;
     decode_lean_kernel<<<grid, 64 * rows::NKV, 0, s>>>(p);
-    combine_lean_kernel<<<dim3(rows::NKV, batch), 512, 0, s>>>(p, grid);
+    combine_lean_kernel<<<dim3(rows::NKV, batch), 64 * R, 0, s>>>(p, grid);
     return check_launch(fn);
   }
 
