@@ -1103,19 +1103,28 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   for (int k = 0; k < DPL; ++k) acc[0][k] = f32x4{0.f, 0.f, 0.f, 0.f};
   int seg_j0 = 0;  // range index of the current segment's first tile
   int seg_T0 = 0;  // its first token
+  int stores_prev = 0, stores_prev2 = 0;  // epilogue stores of iterations j-1 and j-2 (lower bounds)
   for (int j = 0; j < n; ++j) {
     const TileDesc d = dA;
     char* buf = lds + (j & 1) * rows::BUF_BYTES;
-    // This wave's copies of tile j have landed once at most the next tile's group is in flight:
-    // 16 row copies, plus 4 Q copies when that tile starts a segment (stores issued later only
-    // make the wait stricter).
-    if (j + 1 >= n)
+    // This wave's copies of tile j have landed once at most the operations issued after them are
+    // outstanding (vmcnt retires in order): the epilogue stores of iteration j-2 (issued after
+    // group j), group j+1 (16 row copies, + 4 Q copies when tile j+1 starts a segment) and the
+    // epilogue stores of iteration j-1.  Store counts are lower bounds: the wait is never looser
+    // than it must be, and no longer stalls on the next tile after a segment ends.
+    if (j + 1 >= n) {
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    else if (dB.T0 == 0)
-      __builtin_amdgcn_s_waitcnt(0x4F74);  // vmcnt(20)
-    else
-      __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16)
-    raw_barrier();                         // ... and every other wave's
+    } else {
+      switch ((dB.T0 == 0 ? 20 : 16) + stores_prev + stores_prev2) {
+        case 20: __builtin_amdgcn_s_waitcnt(0x4F74); break;  // vmcnt(20)
+        case 24: __builtin_amdgcn_s_waitcnt(0x4F78); break;  // vmcnt(24)
+        case 28: __builtin_amdgcn_s_waitcnt(0x4F7C); break;  // vmcnt(28)
+        case 32: __builtin_amdgcn_s_waitcnt(0x8F70); break;  // vmcnt(32)
+        case 36: __builtin_amdgcn_s_waitcnt(0x8F74); break;  // vmcnt(36)
+        default: __builtin_amdgcn_s_waitcnt(0x4F70); break;  // vmcnt(16)
+      }
+    }
+    raw_barrier();  // ... and every other wave's
     if (j == 0 || d.T0 == 0) {
       // a segment starts: its Q operand, row limits and a fresh softmax state
       rows_read_q(p, buf, h, qf);
@@ -1153,8 +1162,11 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     }
     if (d.T0 < d.L) compute_tile<HD, 1, true>(p, tl, d.T0, qf, lim, lim_min, m_run, l_run, acc);
 
+    stores_prev2 = stores_prev;
+    stores_prev = 0;
     if (j + 1 < n && d.T0 + rows::TILE < d.L) continue;  // the segment goes on
-    // ---- segment epilogue: wave h owns head h's rows li < R ----
+    // ---- segment epilogue: wave h owns head h's rows li < R (4 stores, or 8 + 1 for a partial) ----
+    stores_prev = seg_T0 == 0 && d.T0 + rows::TILE >= d.L ? 4 : 8;
     const float lsum = sum_over_quads(l_run[0]);
     if (li >= p.R) {
       // padding rows: nothing to write
