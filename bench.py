@@ -1,17 +1,22 @@
 """Benchmark: paged decode attention (append + attention) at the Qwen2.5-7B shape, batch 32.
 
-Workload (the metric's configuration): 28 layers, 28 query / 4 KV heads,
-head_dim 128, bf16, 256-token pages in a 2043-page (30 GB) pool fragmented by freeing a seeded 40%
-of it, 32 sequences with context lengths lognormal(median 1500, sigma 1) clipped to [16, 32768].
-One step = for each of the 28 layers, append one new K/V row per sequence and run paged decode
-attention over it (prism_amd.flash_attn_with_kvcache, the drop-in for Prism's per-layer call at
-engine/executor.py:260-261).  Inputs are resident in HBM before timing; every layer reads its own
-cache, so a step streams the whole working set and the 256 MB Infinity Cache cannot serve it.
+Default workload (the metric's configuration): 28 layers, 28 query /
+4 KV heads, head_dim 128, bf16, 256-token pages in a 2043-page (30 GB) pool fragmented by freeing
+a seeded 40% of it, 32 sequences with context lengths lognormal(median 1500, sigma 1) clipped to
+[16, 32768].  One step = for each of the 28 layers, append one new K/V row per sequence and run
+paged decode attention over it (prism_amd.flash_attn_with_kvcache, the drop-in for Prism's
+per-layer call at engine/executor.py:260-261).  Inputs are resident in HBM before timing; every
+layer reads its own cache, so a step streams the whole working set and the 256 MB Infinity Cache
+cannot serve it.
 
 The step is captured once in a HIP graph and replayed (as Prism's executor runs decode); HIP events
 on the replay stream bracket the K timed replays.  Prints one JSON line: value = algorithmic HBM
-bytes per step / step time (GB/s), the per-call roofline (step time / 28 calls) and a CPU baseline
+bytes per step / step time (GB/s), the per-call roofline (step time / layers) and a CPU baseline
 (the oracle's torch-CPU reference path on a bounded sample of the same workload, N=1 only).
+
+--workload config2 / config4 / config5 measures the other configurations the same way (decode at
+b=8 ctx 2048; 14B chunked prefill, MFMA-bound, in TFLOP/s; 7B shared-prefix speculative verify,
+plus its copy-on-write and a compaction of every live page into a fresh pool).
 """
 from __future__ import annotations
 
@@ -27,6 +32,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+TRAFFIC_PROFILE = ROOT / "profiles" / "decode_config3_traffic.md"
 
 
 def parse():
@@ -35,24 +42,23 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--workload", choices=["config2", "config3", "config4", "config5"], default="config3")
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = library choice)")
-    ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--layers", type=int, default=0, help="layers (0 = the model's)")
     ap.add_argument("--merge", choices=["auto", "two-pass", "fused"], default="auto",
-                    help="split-K merge: library choice, second launch, or inside the attention launch")
+                    help="split-K merge of the per-head kernel: library choice, second launch, in-launch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=4, help="layers in the CPU baseline sample")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
-                    help="after timing, gather this many MiB of pages once (counter calibration)")
+                    help="after timing, copy this many MiB of pages once (counter calibration)")
     return ap.parse_args()
-
-
-TRAFFIC_PROFILE = ROOT / "profiles" / "decode_config3_traffic.md"
 
 
 def profiled_traffic(args, w):
     """HBM bytes per call from the committed FETCH_SIZE / WRITE_SIZE counter passes over this same
     workload (default seed, 28 layers, library-chosen kernel); None for any other configuration."""
-    if args.seed != 0 or w.layers != 28 or args.split or args.merge != "auto" or not TRAFFIC_PROFILE.exists():
+    if (args.workload != "config3" or args.seed != 0 or w.layers != 28 or args.split or args.merge != "auto"
+            or not TRAFFIC_PROFILE.exists()):
         return None, None
     for line in TRAFFIC_PROFILE.read_text().splitlines():
         if line.startswith("traffic_bytes_per_call:"):
@@ -60,9 +66,8 @@ def profiled_traffic(args, w):
     return None, None
 
 
-def cpu_baseline(w, n_layers: int) -> dict:
+def cpu_baseline(w, n_layers: int, metric_unit: str) -> dict:
     """The oracle's torch-CPU path (index_select page gather + fp32 SDPA) on n_layers of the workload."""
-    import numpy as np
     import torch
 
     from oracle import paged_attention as pa
@@ -73,7 +78,7 @@ def cpu_baseline(w, n_layers: int) -> dict:
     bt = w.block_table.cpu()
     sl = w.cache_seqlens.cpu()
     # keep only the referenced pages on the host, with the block table remapped onto them
-    used = sorted({int(p) for b in range(w.batch) for p in bt[b, : -(-(int(sl[b]) + 1) // kv.page_size)]})
+    used = sorted({int(p) for b in range(w.batch) for p in bt[b, : -(-(int(sl[b]) + w.s_q) // kv.page_size)]})
     remap = torch.full((kv.max_pages,), 0, dtype=torch.int64)
     remap[torch.tensor(used)] = torch.arange(len(used))
     bt_host = remap[bt.long()].to(torch.int32)
@@ -87,31 +92,105 @@ def cpu_baseline(w, n_layers: int) -> dict:
         for kc, vc, q, k, v in layers:
             pa.flash_attn_cpu(q, kc, vc, k, v, cache_seqlens=sl, block_table=bt_host, causal=True)
 
-    for _ in range(3):
+    reps = 5 if w.s_q == 1 else 2
+    warm = min(3, reps)
+    for _ in range(warm):
         run()
     times = []
-    for _ in range(5):
+    for _ in range(reps):
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    per_layer = med / n_layers
-    bytes_layer = w.decode_bytes_per_layer()
+    per_layer = statistics.median(times) / n_layers
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
             model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
     except OSError:
         pass
+    value = (w.decode_bytes_per_layer() / per_layer / 1e9 if metric_unit == "GB/s"
+             else w.attention_flops_per_layer() / per_layer / 1e12)
     return {
-        "value": round(bytes_layer / per_layer / 1e9, 3),
-        "unit": "GB/s",
+        "value": round(value, 4),
+        "unit": metric_unit,
         "cores": cores,
         "kind": "port",
         "us_per_step": round(per_layer * w.layers * 1e6, 1),
         "sample": f"{n_layers} of {w.layers} layers, all {w.batch} sequences, referenced pages only; "
-                  f"3 warm-ups, median of 5; torch {torch.__version__} CPU, {model}",
+                  f"{warm} warm-ups, median of {reps}; torch {torch.__version__} CPU, {model}",
     }
+
+
+def time_graph(fn, args, dev) -> float:
+    """Capture fn() once in a HIP graph and replay it; HIP events on the replay stream bracket the
+    K timed replays.  Returns ms per replay."""
+    import torch
+
+    fn()  # eager call: sizes the split-K workspace before capture
+    torch.cuda.synchronize()
+    cap = torch.cuda.Stream(device=dev)
+    cap.wait_stream(torch.cuda.current_stream(dev))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cap):
+        fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=cap):
+            fn()
+    torch.cuda.current_stream(dev).wait_stream(cap)
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    print(f"[bench] warmup done ({args.warmup} graph replays)", file=sys.stderr, flush=True)
+    stream = torch.cuda.current_stream(dev)
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record(stream)
+    for _ in range(args.steps):
+        graph.replay()
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    return t_start.elapsed_time(t_end) / args.steps
+
+
+def time_eager(fn, reps: int) -> float:
+    """ms per call of fn() (one launch), HIP events around reps back-to-back calls."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def config5_page_ops(prism_amd, w, dev) -> dict:
+    """Copy-on-write of the shared boundary page into every child (one launch) and compaction of
+    every live page into a fresh pool (one launch), each timed on its own."""
+    kv = w.kv
+    L = w.layers
+    out = {}
+    fill = w.meta["boundary_fill"]
+    if fill:
+        bidx = w.meta["shared_prefix"] // kv.page_size
+        first = kv.seq_pages[w.seq_ids[0]][bidx]
+        dst = [kv.seq_pages[s][bidx] for s in w.seq_ids[1:]]
+        src = [first] * len(dst)   # the same copy shape: fill slots of one page into every other child
+        ms = time_eager(lambda: prism_amd.copy_pages(kv, kv, src, dst, [fill] * len(dst)), 20)
+        nbytes = 2 * len(dst) * fill * kv.num_kv_heads * kv.head_dim * 2 * 2 * L
+        out["copy_on_write"] = {"pages": len(dst), "fill_slots": fill, "us": round(ms * 1e3, 2), "bytes": nbytes,
+                                "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    live = kv.live_pages()
+    fresh = prism_amd.FlashAttnKVCache(L, kv.num_kv_heads, kv.head_dim, len(live), kv.page_size, str(dev))
+    ms = time_eager(lambda: prism_amd.copy_pages(kv, fresh, live, list(range(len(live))), None), 5)
+    nbytes = 2 * len(live) * kv.bytes_per_page * 2 * L
+    out["compaction"] = {"pages": len(live), "us": round(ms * 1e3, 1), "bytes": nbytes,
+                         "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    return out
 
 
 def main() -> int:
@@ -128,61 +207,30 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    print(f"[bench] building config3 workload (layers={args.layers}, seed={args.seed})", file=sys.stderr, flush=True)
-    w = workloads.config3(dev, seed=args.seed, layers=args.layers)
+    print(f"[bench] building {args.workload} workload (seed={args.seed})", file=sys.stderr, flush=True)
+    w = getattr(workloads, args.workload)(dev, seed=args.seed, layers=args.layers or None)
     L = w.layers
     outs = [torch.empty_like(q) for q in w.q]
     kv = w.kv
-
-    def call(l):
-        prism_amd.flash_attn_with_kvcache(w.q[l], kv.k_caches[l], kv.v_caches[l], k=w.k[l], v=w.v[l],
-                                          cache_seqlens=w.cache_seqlens, block_table=w.block_table,
-                                          causal=True, out=outs[l], split_tokens=args.split,
-                                          two_pass={"auto": None, "two-pass": True, "fused": False}[args.merge])
+    two_pass = {"auto": None, "two-pass": True, "fused": False}[args.merge]
 
     def step():
         for l in range(L):
-            call(l)
+            prism_amd.flash_attn_with_kvcache(w.q[l], kv.k_caches[l], kv.v_caches[l], k=w.k[l], v=w.v[l],
+                                              cache_seqlens=w.cache_seqlens, block_table=w.block_table,
+                                              causal=True, out=outs[l], split_tokens=args.split,
+                                              two_pass=two_pass)
 
-    # An eager step sizes the split-K workspace; the step is then captured in a HIP graph and
-    # replayed, as Prism's executor runs decode (engine/executor.py:272-310, :358-360).
-    step()
-    torch.cuda.synchronize()
-    cap = torch.cuda.Stream(device=dev)
-    cap.wait_stream(torch.cuda.current_stream(dev))
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(cap):
-        step()
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph, stream=cap):
-            step()
-    torch.cuda.current_stream(dev).wait_stream(cap)
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    print(f"[bench] warmup done ({args.warmup} graph replays)", file=sys.stderr, flush=True)
-
-    # HIP events on the replay stream bracket exactly the K timed steps.
-    stream = torch.cuda.current_stream(dev)
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_start.record(stream)
-    for _ in range(args.steps):
-        graph.replay()
-    t_end.record(stream)
-    torch.cuda.synchronize()
-    step_ms = t_start.elapsed_time(t_end) / args.steps
-    avg_call_us = step_ms * 1e3 / L
+    step_ms = time_graph(step, args, dev)
     status = prism_amd.read_status(dev)
     if status:
         print(f"[bench] WARNING: kernel status flags {status}", file=sys.stderr)
-
+    call_us = step_ms * 1e3 / L
     bytes_layer = w.decode_bytes_per_layer()
-    bytes_step = bytes_layer * L
-    value = bytes_step / (step_ms * 1e-3) / 1e9
-    achieved = bytes_layer / (avg_call_us * 1e-6) / 1e9
-    print(f"[bench] step {step_ms * 1e3:.1f} us, call avg {avg_call_us:.2f} us, {achieved:.0f} GB/s",
+    flops_layer = w.attention_flops_per_layer()
+    gbs = bytes_layer / (call_us * 1e-6) / 1e9
+    tflops = flops_layer / (call_us * 1e-6) / 1e12
+    print(f"[bench] step {step_ms * 1e3:.1f} us, call avg {call_us:.2f} us, {gbs:.0f} GB/s, {tflops:.1f} TFLOP/s",
           file=sys.stderr, flush=True)
 
     if args.copy_probe_mib:
@@ -194,49 +242,80 @@ def main() -> int:
         print(f"[bench] copy probe: {len(src) * kv.bytes_per_page * 2 * L} bytes read and written by "
               f"copy_pages_kernel", file=sys.stderr, flush=True)
 
-    traffic, traffic_src = profiled_traffic(args, w)
-    result = {
-        "metric": "paged decode attn HBM GB/s (% of peak) + us/step, Qwen2.5-7B shape b=32",
-        "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(step_ms, 4),
-        "us_per_step": round(step_ms * 1e3, 1),
-        "tokens_per_s": round(w.batch / (step_ms * 1e-3), 1),
-        "pct_of_peak_hbm": round(100 * value / HBM_PEAK_GBS, 2),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
-        "config": {
-            "workload": "config3: Qwen2.5-7B paged decode (append + attention), 28 layers, b=32, "
-                        "ctx lognormal(1500, 1) in [16, 32768], 2043-page 30 GB pool, 40% churn",
-            "batch": w.batch, "layers": L, "n_heads": w.n_heads, "n_kv": kv.num_kv_heads,
-            "head_dim": kv.head_dim, "page_size": kv.page_size, "pool_pages": kv.max_pages,
-            "sum_ctx": int(w.ctx.sum()), "max_ctx": int(w.ctx.max()), "seed": args.seed,
-            "split_tokens": args.split or "auto", "merge": args.merge,
-        },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "traffic_source": traffic_src,
-            "kernel": "one pkv_decode_attn call = decode_lean_kernel (append + balanced paged attention, "
-                      "split-K partials) + combine_lean_kernel (merge); HIP events around K graph replays "
-                      "of the 28-call step, per call = step / 28",
-            "bytes_per_call": bytes_layer,
-            "avg_call_us": round(avg_call_us, 3),
-        },
+    common = {
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4), "us_per_step": round(step_ms * 1e3, 1),
+        "tokens_per_s": round(w.batch * w.s_q / (step_ms * 1e-3), 1),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
     }
+    cfg = {"workload": "", "batch": w.batch, "layers": L, "n_heads": w.n_heads, "n_kv": kv.num_kv_heads,
+           "head_dim": kv.head_dim, "page_size": kv.page_size, "pool_pages": kv.max_pages, "s_q": w.s_q,
+           "sum_ctx": int(w.ctx.sum()), "max_ctx": int(w.ctx.max()), "seed": args.seed,
+           "split_tokens": args.split or "auto", "merge": args.merge}
+    per_call = f"HIP events around K graph replays of the {L}-call step, per call = step / {L}"
+    if args.workload in ("config2", "config3"):
+        traffic, traffic_src = profiled_traffic(args, w)
+        if args.workload == "config3":
+            metric = "paged decode attn HBM GB/s (% of peak) + us/step, Qwen2.5-7B shape b=32"
+            cfg["workload"] = ("config3: Qwen2.5-7B paged decode (append + attention), 28 layers, b=32, ctx "
+                               "lognormal(1500, 1) in [16, 32768], 2043-page 30 GB pool, 40% churn")
+        else:
+            metric = "paged decode attn HBM GB/s (% of peak) + us/step, Qwen2.5-7B shape b=8 ctx 2048"
+            cfg["workload"] = ("config2: Qwen2.5-7B paged decode (append + attention), 28 layers, b=8, ctx 2048, "
+                               "2043-page 30 GB pool")
+        result = {
+            "metric": metric, "value": round(bytes_layer * L / (step_ms * 1e-3) / 1e9, 2), "unit": "GB/s",
+            **common, "pct_of_peak_hbm": round(100 * gbs / HBM_PEAK_GBS, 2), "config": cfg,
+            "roofline": {
+                "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
+                "kernel": "one pkv_decode_attn call = decode_lean_kernel (append + balanced paged attention, "
+                          "split-K partials) + combine_lean_kernel (merge); " + per_call,
+                "bytes_per_call": bytes_layer, "avg_call_us": round(call_us, 3),
+            },
+        }
+        unit = "GB/s"
+    elif args.workload == "config4":
+        cfg["workload"] = ("config4: Qwen2.5-14B varlen chunked prefill over paged KV, 48 layers, b=8 chunks of "
+                           "512 appended onto prefixes ~U{0..4096}, causal, 596-page 30 GB pool")
+        result = {
+            "metric": "chunked prefill attn TFLOP/s (% of bf16 MFMA peak), Qwen2.5-14B shape b=8 chunk 512",
+            "value": round(flops_layer * L / (step_ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", **common,
+            "config": cfg,
+            "roofline": {
+                "bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                "kernel": "one pkv_prefill_attn call = append_kernel + prefill_kernel<128,2,4>; " + per_call,
+                "flops_per_call": flops_layer, "bytes_per_call": bytes_layer, "avg_call_us": round(call_us, 3),
+                "hbm_gbs": round(gbs, 1),
+            },
+        }
+        unit = "TFLOP/s"
+    else:
+        cfg["workload"] = ("config5: Qwen2.5-7B shared 2048-token prefix (ref-counted, copy-on-write boundary "
+                           "page) + speculative verify of 5 draft tokens, 28 layers, b=64, suffix ~U{0..1024}")
+        cfg.update({k: v for k, v in w.meta.items() if k != "shape"})
+        page_ops = config5_page_ops(prism_amd, w, dev)
+        result = {
+            "metric": "speculative verify attn HBM GB/s (% of peak) + MFMA %, Qwen2.5-7B shape b=64 draft 5",
+            "value": round(bytes_layer * L / (step_ms * 1e-3) / 1e9, 2), "unit": "GB/s", **common,
+            "config": cfg,
+            "roofline": {
+                "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "mfma_tflops": round(tflops, 2), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                "kernel": "one pkv_decode_attn call (s_q=5, 35 query rows per KV head) = decode_kernel<128,3,2> "
+                          "with in-launch split-K merge; bytes count every sequence's reads of the shared "
+                          "prefix; " + per_call,
+                "bytes_per_call": bytes_layer, "flops_per_call": flops_layer, "avg_call_us": round(call_us, 3),
+            },
+            "page_ops": page_ops,
+        }
+        unit = "GB/s"
     if not args.no_cpu_baseline:
-        print(f"[bench] cpu baseline on {args.cpu_layers} layers", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(w, min(args.cpu_layers, L))
+        n_cpu = min(args.cpu_layers if args.workload == "config3" else 1, L)
+        print(f"[bench] cpu baseline on {n_cpu} layers", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(w, n_cpu, unit)
     print(json.dumps(result), flush=True)
     return 0
 
