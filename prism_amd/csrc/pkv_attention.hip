@@ -1362,6 +1362,264 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(const AttnParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// Chunked prefill with LDS-staged KV tiles (head_dim 128, pages of >= 32 rows): grid (row block,
+// KV head, sequence).  The W waves of a workgroup own 16*NT consecutive query rows each (row =
+// j * g + head-in-group, so a block spans a few query positions of every head of the group) and
+// share each 32-token K / V tile of their KV head: the workgroup copies a tile into LDS once
+// (16 global_load_lds_dwordx4 of 1 KiB, 16 / W per wave), NBUF tiles in flight, and every wave
+// reads its MFMA operands from there (chunks XOR-swizzled by swz(row) as in the decode kernel).
+// The block walks keys up to its last row's last visible key; rows that see fewer keys are masked
+// inside the tiles that cross their limit.  No split-K: every wave writes its own rows.
+// ---------------------------------------------------------------------------------------------
+namespace pf {
+constexpr int HD = 128;
+constexpr int ROW = HD * 2;            // one KV head's slice of a token row: 256 B
+constexpr int TILE = 32;
+constexpr int KV_BYTES = TILE * ROW;   // 8 KiB of K (or V) per tile
+constexpr int BUF = 2 * KV_BYTES;      // K | V
+}  // namespace pf
+
+template <int OPS, int NBUF>
+__device__ __forceinline__ void pf_wait(int ahead) {
+  // at most `ahead` later tiles' copies (OPS per tile for this wave) may stay in flight
+  static_assert(OPS * (NBUF - 1) <= 15, "vmcnt immediate");
+  switch (ahead) {
+    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 1: __builtin_amdgcn_s_waitcnt(0x0F70 | OPS); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0x0F70 | (NBUF > 2 ? 2 * OPS : OPS)); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F70 | (OPS * (NBUF - 1))); break;
+  }
+}
+
+// Online-softmax update of a wave's 16*NT prefill rows with one 32-token tile, arranged for
+// instruction-level parallelism across the N tiles: every S^T product first (NT x 2 independent
+// MFMA chains), then the softmax of all tiles with one wave-uniform rescale test, then every PV
+// product.  The row max is taken on raw scores (the scale is positive) and the scale is folded
+// into the exponent's FMA.  P is rounded to bf16 once (prefill has no MFMA headroom to spare).
+template <int NT>
+__device__ __forceinline__ void compute_tile_prefill(const AttnParams& p, const KVTile<128>& tl, int T0,
+                                                     const bf16x8 (&qf)[NT][4], const int (&lim)[NT], int lim_min,
+                                                     float (&m_run)[NT], float (&l_run)[NT], f32x4 (&acc)[NT][8]) {
+  constexpr int DPL = 8;
+  const int lane = threadIdx.x & 63;
+  const int lq = lane >> 4;
+  f32x4 s[NT][2];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      s[nt][a] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        s[nt][a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, tl.kr[a][kk]), qf[nt][kk],
+                                                           s[nt][a], 0, 0, 0);
+    }
+  bf16x8 vt[DPL];
+#pragma unroll
+  for (int n = 0; n < DPL; ++n) {
+    const int w = n >> 1;
+    const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
+    u32x4 pk;
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) pk[pp] = __builtin_amdgcn_perm(tl.vr[2 * pp + 1].w[w], tl.vr[2 * pp].w[w], sel);
+    vt[n] = __builtin_bit_cast(bf16x8, pk);
+  }
+  if (T0 + 31 > lim_min) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (T0 + 8 * lq + 4 * a + r > lim[nt]) s[nt][a][r] = -INFINITY;
+  }
+  float mx[NT];
+  bool grow_any = false;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    float m = fmaxf(fmaxf(fmaxf(s[nt][0][0], s[nt][0][1]), fmaxf(s[nt][0][2], s[nt][0][3])),
+                    fmaxf(fmaxf(s[nt][1][0], s[nt][1][1]), fmaxf(s[nt][1][2], s[nt][1][3])));
+    mx[nt] = max_over_quads(m) * p.scale_log2;
+    grow_any |= mx[nt] > m_run[nt] + kRescaleSlack;
+  }
+  if (__any(grow_any)) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const float m_new = mx[nt] > m_run[nt] + kRescaleSlack ? mx[nt] : m_run[nt];
+      const float alpha = fast_exp2(m_run[nt] - m_new);
+      l_run[nt] *= alpha;
+#pragma unroll
+      for (int n = 0; n < DPL; ++n) acc[nt][n] *= alpha;
+      m_run[nt] = m_new;
+    }
+  }
+  bf16x8 pb[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const float neg_m = (m_run[nt] == -INFINITY) ? 0.f : -m_run[nt];
+    float psum = 0.f;
+    u32x4 pk;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const float p0 = fast_exp2(fmaf(s[nt][e >> 2][e & 3], p.scale_log2, neg_m));
+      const float p1 = fast_exp2(fmaf(s[nt][e >> 2][(e & 3) + 1], p.scale_log2, neg_m));
+      psum += p0 + p1;
+      pk[e >> 1] = pack_bf16x2(p0, p1);
+    }
+    l_run[nt] += psum;
+    pb[nt] = __builtin_bit_cast(bf16x8, pk);
+  }
+#pragma unroll
+  for (int n = 0; n < DPL; ++n)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      acc[nt][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[n], pb[nt], acc[nt][n], 0, 0, 0);
+}
+
+template <int NT, int W, int NBUF, int SUB>
+__global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p) {
+  constexpr int HD = pf::HD;
+  constexpr int DPL = HD / 16;
+  constexpr int OPS = 16 / W * SUB;  // copies per wave per stage (SUB tiles of 32 tokens)
+  static_assert(16 % W == 0, "waves must split the 16 copies of a tile");
+  __shared__ __attribute__((aligned(16))) char lds[NBUF * SUB * pf::BUF];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15;
+  const int lq = lane >> 4;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+
+  int c, L;
+  seq_lengths(p, b, c, L);
+  SeqView sv;
+  sv.b = b;
+  sv.h = h;
+  sv.c = c;
+  sv.t_end = L;
+  sv.bt = p.block_table + int64_t(b) * p.bt_stride;
+
+  const int blk_row0 = blockIdx.x * W * 16 * NT;
+  if (blk_row0 >= p.R) return;
+  const int row0 = blk_row0 + wave * 16 * NT;
+  // the block's last row sees the most keys (rows increase with j)
+  const int blk_last = min(blk_row0 + W * 16 * NT, p.R) - 1;
+  const int t_stop = p.causal ? min(L, L - p.s_q + blk_last / p.g + 1) : L;
+  const int n_tiles = t_stop > 0 ? (t_stop + pf::TILE - 1) / pf::TILE : 0;
+  const int n_stages = (n_tiles + SUB - 1) / SUB;
+
+  bf16x8 qf[NT][HD / 32];
+  int lim[NT];
+  load_q<HD, NT>(p, sv, L, row0, qf, lim);
+  int lim_min = 0x7fffffff;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) lim_min = min(lim_min, lim[nt] < 0 ? 0x7fffffff : lim[nt]);
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) lim_min = min(lim_min, __shfl_xor(lim_min, off, 64));
+  lim_min = __builtin_amdgcn_readfirstlane(lim_min);
+
+  BtWindow btw;
+  bt_window_load(p, sv, 0, btw);
+  const int row_elems = p.n_kv * HD;
+  // Stage st holds tiles SUB*st .. SUB*st + SUB-1 (the last stage repeats its last real tile so
+  // every stage issues the same number of copies).  Copy instruction i of a tile: K (i < 8) or V
+  // rows 4 (i % 8) .. +3, lane l -> row + l / 16, LDS chunk l % 16 <- global chunk (l % 16) ^ swz(row).
+  auto issue = [&](int st) {
+    char* stage = lds + (st % NBUF) * SUB * pf::BUF;
+#pragma unroll
+    for (int u = 0; u < SUB; ++u) {
+      const int T0 = min(st * SUB + u, n_tiles - 1) * pf::TILE;
+      const int pid = bt_page(p, sv, T0 >> p.log2_page, btw);
+      const bool ok = unsigned(pid) < unsigned(p.num_pages);
+      if (!ok && T0 < L && lane == 0) flag_status(p.status, PKV_STATUS_BAD_PAGE);
+      const int64_t off = int64_t(ok ? pid : 0) * p.page_stride +
+                          int64_t(T0 & ((1 << p.log2_page) - 1)) * row_elems + h * HD;
+      char* buf = stage + u * pf::BUF;
+#pragma unroll
+      for (int k = 0; k < 16 / W; ++k) {
+        const int i = wave + k * W;
+        const int r = 4 * (i & 7) + (lane >> 4);
+        const int gc = (lane & 15) ^ rows::swz(r);
+        const uint16_t* src = (i < 8 ? p.k_cache : p.v_cache) + off + int64_t(r) * row_elems + gc * 8;
+        __builtin_amdgcn_global_load_lds(src, (rows::lds_void*)(buf + (i >= 8 ? pf::KV_BYTES : 0) + (i & 7) * 1024),
+                                         16, 0, 0);
+      }
+    }
+  };
+  for (int st = 0; st < NBUF && st < n_stages; ++st) issue(st);
+
+  float m_run[NT], l_run[NT];
+  f32x4 acc[NT][DPL];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    m_run[nt] = -INFINITY;
+    l_run[nt] = 0.f;
+#pragma unroll
+    for (int n = 0; n < DPL; ++n) acc[nt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int st = 0; st < n_stages; ++st) {
+    pf_wait<OPS, NBUF>(min(NBUF - 1, n_stages - 1 - st));
+    raw_barrier();
+#pragma unroll
+    for (int u = 0; u < SUB; ++u) {
+      const int t = st * SUB + u;
+      if (t >= n_tiles) break;
+      const int T0 = t * pf::TILE;
+      const char* buf = lds + ((st % NBUF) * SUB + u) * pf::BUF;
+      KVTile<HD> tl;
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int r = 8 * (li >> 2) + 4 * a + (li & 3);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+          tl.kr[a][kk] = *reinterpret_cast<const u32x4*>(buf + r * pf::ROW + (((4 * kk + lq) ^ rows::swz(r)) << 4));
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int r = 8 * lq + e;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(buf + pf::KV_BYTES + r * pf::ROW + ((li ^ rows::swz(r)) << 4));
+#pragma unroll
+        for (int w = 0; w < 4; ++w) tl.vr[e].w[w] = v[w];
+      }
+      if (T0 + pf::TILE > L) {
+        // rows past the sequence: P = 0 must not meet a stale NaN
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const bool keep = T0 + 8 * lq + e < L;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) tl.vr[e].w[w] = keep ? tl.vr[e].w[w] : 0u;
+        }
+      }
+      if (row0 < p.R) compute_tile_prefill<NT>(p, tl, T0, qf, lim, lim_min, m_run, l_run, acc);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the stage are done
+    raw_barrier();                       // the stage's buffer is free
+    if (st + NBUF < n_stages) issue(st + NBUF);
+  }
+  if (row0 >= p.R) return;
+
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int row = row0 + li + 16 * nt;
+    const float lsum = sum_over_quads(l_run[nt]);
+    if (row < p.R) {
+      const int j = row / p.g;
+      const int hq = row - j * p.g;
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      uint16_t* dst = p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + 4 * DPL * lq;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        u32x4 ov;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[nt][2 * k][r] * inv, acc[nt][2 * k + 1][r] * inv);
+        st16(dst + DPL * r, ov);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------------------------
 // Default KV range per workgroup of decode_kernel (decode_lean_kernel splits by range instead).
@@ -1507,6 +1765,27 @@ static void launch_decode_hd(const AttnParams& p, int batch, hipStream_t stream)
 constexpr int kPrefillNT = 2;
 constexpr int kPrefillW = 4;
 
+#ifndef PKV_PREFILL_LDS_NT
+#define PKV_PREFILL_LDS_NT 2
+#endif
+#ifndef PKV_PREFILL_LDS_W
+#define PKV_PREFILL_LDS_W 4
+#endif
+#ifndef PKV_PREFILL_LDS_NBUF
+#define PKV_PREFILL_LDS_NBUF 2
+#endif
+
+#ifndef PKV_PREFILL_LDS_SUB
+#define PKV_PREFILL_LDS_SUB 1
+#endif
+
+static void launch_prefill_lds(const AttnParams& p, int batch, hipStream_t stream) {
+  constexpr int NT = PKV_PREFILL_LDS_NT, W = PKV_PREFILL_LDS_W;
+  constexpr int rows_per_wg = 16 * NT * W;
+  dim3 grid((p.R + rows_per_wg - 1) / rows_per_wg, p.n_kv, batch);
+  prefill_lds_kernel<NT, W, PKV_PREFILL_LDS_NBUF, PKV_PREFILL_LDS_SUB><<<grid, 64 * W, 0, stream>>>(p);
+}
+
 template <int HD>
 static void launch_prefill_hd(const AttnParams& p, int batch, hipStream_t stream) {
   constexpr int rows_per_wg = 16 * kPrefillNT * kPrefillW;
@@ -1639,7 +1918,9 @@ extern "C" int pkv_prefill_attn(const void* q, int64_t q_sb, int64_t q_ss, int64
                        page_size, num_pages, max_blocks, status, s);
     if (rc) return rc;
   }
-  if (head_dim == 128)
+  if (head_dim == 128 && page_size >= pf::TILE)
+    launch_prefill_lds(p, batch, s);
+  else if (head_dim == 128)
     launch_prefill_hd<128>(p, batch, s);
   else
     launch_prefill_hd<64>(p, batch, s);
