@@ -304,9 +304,9 @@ def main() -> int:
                 "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                 "mfma_tflops": round(tflops, 2), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-                "kernel": "one pkv_decode_attn call (s_q=5, 35 query rows per KV head) = decode_kernel<128,3,2> "
-                          "with in-launch split-K merge; bytes count every sequence's reads of the shared "
-                          "prefix; " + per_call,
+                "kernel": "one pkv_decode_attn call (s_q=5, 35 query rows per KV head) = decode_lean_kernel<3> "
+                          "(balanced tile ranges, 3 MFMA row tiles per wave) + combine_lean_kernel; bytes count "
+                          "every sequence's reads of the shared prefix; " + per_call,
                 "bytes_per_call": bytes_layer, "flops_per_call": flops_layer, "avg_call_us": round(call_us, 3),
             },
             "page_ops": page_ops,

@@ -96,7 +96,7 @@ size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, i
  * 1/sqrt(head_dim)); softmax and accumulation are fp32, out is bf16 [batch, s_q, n_heads,
  * head_dim] with the given strides.  A query row with no visible key gets zeros.
  * Two kernels serve the call.  Where head_dim = 128, n_kv = 4, page_size >= 32,
- * s_q * n_heads / n_kv <= 16 and batch <= 256 (the Qwen2.5-7B decode shape), split_tokens = 0 and
+ * batch <= 256 (the Qwen2.5-7B decode and verify shapes), split_tokens = 0 and
  * neither PKV_DECODE_HEADS nor PKV_DECODE_FUSED_MERGE is set, a balanced kernel gives every
  * workgroup an equal share of all sequences' 32-token KV tiles and a second launch merges the
  * sequences that straddle shares.  Otherwise a per-(sequence, KV head, split) kernel reduces

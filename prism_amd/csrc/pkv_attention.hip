@@ -1066,10 +1066,54 @@ __device__ __forceinline__ void rows_append_from_lds(const AttnParams& p, const 
   }
 }
 
+// s_waitcnt vmcnt(n) for a wave-uniform n, rounded down to a multiple of 4 (a stricter wait) and
+// capped at 60: the immediate must be a constant, so the count selects among the encodings
+// (vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt fields left at "no wait").
+__device__ __forceinline__ void wait_vmcnt_at_most(int n) {
+#define PKV_VMCNT_CASE(k) \
+  case k: __builtin_amdgcn_s_waitcnt(0x0F70 | ((4 * k) & 15) | (((4 * k) >> 4) << 14)); break;
+  switch (min(max(n, 0), 60) >> 2) {
+    PKV_VMCNT_CASE(1) PKV_VMCNT_CASE(2) PKV_VMCNT_CASE(3) PKV_VMCNT_CASE(4) PKV_VMCNT_CASE(5)
+    PKV_VMCNT_CASE(6) PKV_VMCNT_CASE(7) PKV_VMCNT_CASE(8) PKV_VMCNT_CASE(9) PKV_VMCNT_CASE(10)
+    PKV_VMCNT_CASE(11) PKV_VMCNT_CASE(12) PKV_VMCNT_CASE(13) PKV_VMCNT_CASE(14) PKV_VMCNT_CASE(15)
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+  }
+#undef PKV_VMCNT_CASE
+}
+
+// Q^T operand of head h's 16*NT rows of sequence d.b straight from q into registers (load_q's
+// layout; rows >= R get zeros).  Used where NT > 1, whose Q does not fit the LDS buffers.
+template <int NT>
+__device__ __forceinline__ void rows_load_q(const AttnParams& p, const TileDesc& d, int h, bf16x8 (&qf)[NT][4]) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15;
+  const int lq = lane >> 4;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int rr = li + 16 * nt;
+    const int rc = min(rr, p.R - 1);
+    const int jq = rc / p.g;
+    const int hq = rc - jq * p.g;
+    const uint16_t* base = p.q + d.b * p.q_sb + jq * p.q_ss + (h * p.g + hq) * p.q_sh + 8 * lq;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 v = ld16(base + 32 * kk);
+      qf[nt][kk] = __builtin_bit_cast(bf16x8, rr < p.R ? v : u32x4{0u, 0u, 0u, 0u});
+    }
+  }
+}
+
+// NT = 16-row MFMA N tiles per wave: R <= 16 * NT query rows per KV head.  NT = 1 (decode) brings
+// a segment's Q through the LDS buffers with the tile copies; NT > 1 (speculative verify) loads Q
+// into registers at the segment start and rounds P to bf16 once (its MFMA work is NT times
+// decode's, so it gives up the hi + lo split).
+template <int NT>
 __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p) {
   constexpr int HD = rows::HD;
   constexpr int DPL = HD / 16;
-  __shared__ __attribute__((aligned(16))) char lds[2 * rows::BUF_BYTES];
+  constexpr bool kQInLds = NT == 1;
+  constexpr int BUF = kQInLds ? rows::BUF_BYTES : 2 * rows::TILE_BYTES;
+  __shared__ __attribute__((aligned(16))) char lds[2 * BUF];
 
   const int lane = threadIdx.x & 63;
   const int h = threadIdx.x >> 6;  // one wave per KV head
@@ -1088,62 +1132,69 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   tile_window(p, st, s, e, win);
   TileDesc dA = tile_desc(win, s);
   TileDesc dB = dA;
-  rows_issue(p, dA, true, lds);
+  rows_issue(p, dA, kQInLds, lds);
   if (n > 1) {
     dB = tile_desc(win, s + 1);
-    rows_issue(p, dB, dB.T0 == 0, lds + rows::BUF_BYTES);
+    rows_issue(p, dB, kQInLds && dB.T0 == 0, lds + BUF);
   }
 
-  bf16x8 qf[1][HD / 32];
-  int lim[1] = {-1};
+  bf16x8 qf[NT][HD / 32];
+  int lim[NT];
   int lim_min = 0x7fffffff;
-  float m_run[1] = {-INFINITY}, l_run[1] = {0.f};
-  f32x4 acc[1][DPL];
+  float m_run[NT], l_run[NT];
+  f32x4 acc[NT][DPL];
 #pragma unroll
-  for (int k = 0; k < DPL; ++k) acc[0][k] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int nt = 0; nt < NT; ++nt) {
+    lim[nt] = -1;
+    m_run[nt] = -INFINITY;
+    l_run[nt] = 0.f;
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) acc[nt][k] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   int seg_j0 = 0;  // range index of the current segment's first tile
   int seg_T0 = 0;  // its first token
   int stores_prev = 0, stores_prev2 = 0;  // epilogue stores of iterations j-1 and j-2 (lower bounds)
   for (int j = 0; j < n; ++j) {
     const TileDesc d = dA;
-    char* buf = lds + (j & 1) * rows::BUF_BYTES;
+    char* buf = lds + (j & 1) * BUF;
     // This wave's copies of tile j have landed once at most the operations issued after them are
     // outstanding (vmcnt retires in order): the epilogue stores of iteration j-2 (issued after
-    // group j), group j+1 (16 row copies, + 4 Q copies when tile j+1 starts a segment) and the
-    // epilogue stores of iteration j-1.  Store counts are lower bounds: the wait is never looser
-    // than it must be, and no longer stalls on the next tile after a segment ends.
-    if (j + 1 >= n) {
+    // group j), group j+1 (16 row copies, + 4 Q copies when Q goes through LDS and tile j+1
+    // starts a segment) and the epilogue stores of iteration j-1.  Store counts are lower bounds:
+    // the wait is never looser than it must be, and no longer stalls on the next tile after a
+    // segment ends.
+    if (j + 1 >= n)
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    } else {
-      switch ((dB.T0 == 0 ? 20 : 16) + stores_prev + stores_prev2) {
-        case 20: __builtin_amdgcn_s_waitcnt(0x4F74); break;  // vmcnt(20)
-        case 24: __builtin_amdgcn_s_waitcnt(0x4F78); break;  // vmcnt(24)
-        case 28: __builtin_amdgcn_s_waitcnt(0x4F7C); break;  // vmcnt(28)
-        case 32: __builtin_amdgcn_s_waitcnt(0x8F70); break;  // vmcnt(32)
-        case 36: __builtin_amdgcn_s_waitcnt(0x8F74); break;  // vmcnt(36)
-        default: __builtin_amdgcn_s_waitcnt(0x4F70); break;  // vmcnt(16)
-      }
-    }
+    else
+      wait_vmcnt_at_most((kQInLds && dB.T0 == 0 ? 20 : 16) + stores_prev + stores_prev2);
     raw_barrier();  // ... and every other wave's
     if (j == 0 || d.T0 == 0) {
       // a segment starts: its Q operand, row limits and a fresh softmax state
-      rows_read_q(p, buf, h, qf);
+      if constexpr (kQInLds)
+        rows_read_q(p, buf, h, qf);
+      else
+        rows_load_q<NT>(p, d, h, qf);
       seg_j0 = j;
       seg_T0 = d.T0;
-      lim[0] = -1;
-      if (li < p.R) {
-        const int jr = li / p.g;
-        const int last = p.causal ? (d.L - p.s_q + jr) : (d.L - 1);
-        lim[0] = min(last, d.L - 1);
+      lim_min = 0x7fffffff;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int rr = li + 16 * nt;
+        lim[nt] = -1;
+        if (rr < p.R) {
+          const int jr = rr / p.g;
+          const int last = p.causal ? (d.L - p.s_q + jr) : (d.L - 1);
+          lim[nt] = min(last, d.L - 1);
+        }
+        lim_min = min(lim_min, lim[nt] < 0 ? 0x7fffffff : lim[nt]);
+        m_run[nt] = -INFINITY;
+        l_run[nt] = 0.f;
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) acc[nt][k] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-      lim_min = lim[0] < 0 ? 0x7fffffff : lim[0];
 #pragma unroll
       for (int off = 1; off < 16; off <<= 1) lim_min = min(lim_min, __shfl_xor(lim_min, off, 64));
       lim_min = __builtin_amdgcn_readfirstlane(lim_min);
-      m_run[0] = -INFINITY;
-      l_run[0] = 0.f;
-#pragma unroll
-      for (int k = 0; k < DPL; ++k) acc[0][k] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     if (tile_has_new(p, d)) rows_append_from_lds(p, d, buf);
     KVTile<HD> tl;
@@ -1154,47 +1205,63 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
       const int x2 = s + j + 2;
       if (x2 - win.x0 >= 64) tile_window(p, st, x2, e, win);
       const TileDesc d2 = tile_desc(win, x2);
-      rows_issue(p, d2, d2.T0 == 0, buf);
+      rows_issue(p, d2, kQInLds && d2.T0 == 0, buf);
       dA = dB;
       dB = d2;
     } else {
       dA = dB;
     }
-    if (d.T0 < d.L) compute_tile<HD, 1, true>(p, tl, d.T0, qf, lim, lim_min, m_run, l_run, acc);
+    if (d.T0 < d.L) compute_tile<HD, NT, NT == 1>(p, tl, d.T0, qf, lim, lim_min, m_run, l_run, acc);
 
     stores_prev2 = stores_prev;
     stores_prev = 0;
     if (j + 1 < n && d.T0 + rows::TILE < d.L) continue;  // the segment goes on
-    // ---- segment epilogue: wave h owns head h's rows li < R (4 stores, or 8 + 1 for a partial) ----
-    stores_prev = seg_T0 == 0 && d.T0 + rows::TILE >= d.L ? 4 : 8;
-    const float lsum = sum_over_quads(l_run[0]);
-    if (li >= p.R) {
-      // padding rows: nothing to write
-    } else if (seg_T0 == 0 && d.T0 + rows::TILE >= d.L) {
+    // ---- segment epilogue: wave h owns head h's rows li + 16 nt < R (per N tile 4 stores, or
+    // 8 + 1 for a partial; every N tile has a real row) ----
+    const bool whole = seg_T0 == 0 && d.T0 + rows::TILE >= d.L;
+    stores_prev = (whole ? 4 : 8) * NT;
+    float lsum[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) lsum[nt] = sum_over_quads(l_run[nt]);
+    if (whole) {
       // the whole sequence: final output
-      const int jr = li / p.g;
-      const int hq = li - jr * p.g;
-      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-      uint16_t* dst = p.out + d.b * p.o_sb + jr * p.o_ss + (h * p.g + hq) * p.o_sh + 4 * DPL * lq;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        u32x4 ov;
+      for (int nt = 0; nt < NT; ++nt) {
+        const int rr = li + 16 * nt;
+        if (rr < p.R) {
+          const int jr = rr / p.g;
+          const int hq = rr - jr * p.g;
+          const float inv = lsum[nt] > 0.f ? 1.f / lsum[nt] : 0.f;
+          uint16_t* dst = p.out + d.b * p.o_sb + jr * p.o_ss + (h * p.g + hq) * p.o_sh + 4 * DPL * lq;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[0][2 * k][r] * inv, acc[0][2 * k + 1][r] * inv);
-        st16(dst + DPL * r, ov);
+          for (int r = 0; r < 4; ++r) {
+            u32x4 ov;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[nt][2 * k][r] * inv, acc[nt][2 * k + 1][r] * inv);
+            st16(dst + DPL * r, ov);
+          }
+        }
       }
     } else {
       // part of a sequence shared with a neighbouring range: unnormalised partial, merged by the
       // combine launch (the kernel boundary orders these plain stores before its loads)
       const int slot = 2 * int(blockIdx.x) + (seg_j0 == 0 ? 0 : 1);
-      const int64_t row = (int64_t(slot) * rows::NKV + h) * p.R + li;
-      float* dst = p.ws_o + row * HD + 4 * DPL * lq;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        *reinterpret_cast<f32x4*>(dst + DPL * r) = f32x4{acc[0][0][r], acc[0][1][r], acc[0][2][r], acc[0][3][r]};
-        *reinterpret_cast<f32x4*>(dst + DPL * r + 4) = f32x4{acc[0][4][r], acc[0][5][r], acc[0][6][r], acc[0][7][r]};
+      for (int nt = 0; nt < NT; ++nt) {
+        const int rr = li + 16 * nt;
+        if (rr < p.R) {
+          const int64_t row = (int64_t(slot) * rows::NKV + h) * p.R + rr;
+          float* dst = p.ws_o + row * HD + 4 * DPL * lq;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            *reinterpret_cast<f32x4*>(dst + DPL * r) =
+                f32x4{acc[nt][0][r], acc[nt][1][r], acc[nt][2][r], acc[nt][3][r]};
+            *reinterpret_cast<f32x4*>(dst + DPL * r + 4) =
+                f32x4{acc[nt][4][r], acc[nt][5][r], acc[nt][6][r], acc[nt][7][r]};
+          }
+          if (lq == 0) *reinterpret_cast<f32x2*>(p.ws_ml + row * 2) = f32x2{m_run[nt], lsum[nt]};
+        }
       }
-      if (lq == 0) *reinterpret_cast<f32x2*>(p.ws_ml + row * 2) = f32x2{m_run[0], lsum};
     }
   }
 }
@@ -1217,8 +1284,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // Merge of the partials a decode_lean_kernel launch of `grid` workgroups left in the workspace.
-// Workgroup (KV head, sequence), one wave per query row; only sequences whose tiles span more than
-// one range have partials.  Lane u holds part u's (m, l) of the row; for the output lane l owns
+// Workgroup (KV head, sequence, group of 16 query rows), one wave per query row; only sequences
+// whose tiles span more than one range have partials.  Lane u holds part u's (m, l) of the row; for the output lane l owns
 // head-dim elements 2l and 2l + 1 and reads them from every part, all loads of a batch of 32
 // parts in flight at once; the parts' weights reach every lane by v_readlane.  No LDS, no barrier.
 constexpr int kLeanMergeBatch = 32;
@@ -1227,7 +1294,7 @@ __global__ __launch_bounds__(1024) void combine_lean_kernel(const AttnParams p, 
   constexpr int HD = rows::HD;
   const int h = blockIdx.x;
   const int b = blockIdx.y;
-  const int r = threadIdx.x >> 6;  // query row of this wave
+  const int r = int(blockIdx.z) * 16 + int(threadIdx.x >> 6);  // query row of this wave
   const int lane = threadIdx.x & 63;
   if (r >= p.R) return;
 
@@ -1657,12 +1724,16 @@ static size_t ws_bytes(int batch, int R, int n_kv, int head_dim, int64_t max_spl
   return kCounterBytes + (ws_floats_o(batch, R, n_kv, head_dim, max_splits) + rows * 2) * sizeof(float);
 }
 
-// decode_lean_kernel covers the 7B decode shape (head_dim 128, 4 KV heads, pages of >= 32 rows,
-// <= 16 query rows per KV head, <= 256 sequences) and runs there unless the caller fixes
-// split_tokens or asks for decode_kernel (PKV_DECODE_HEADS, PKV_DECODE_FUSED_MERGE).
+// decode_lean_kernel covers the 7B decode and verify shapes (head_dim 128, 4 KV heads, pages of
+// >= 32 rows, <= kLeanMaxRows query rows per KV head, <= 256 sequences) and runs there unless the
+// caller fixes split_tokens or asks for decode_kernel (PKV_DECODE_HEADS, PKV_DECODE_FUSED_MERGE).
+#ifndef PKV_LEAN_MAX_ROWS
+#define PKV_LEAN_MAX_ROWS 64
+#endif
+constexpr int kLeanMaxRows = PKV_LEAN_MAX_ROWS;
 static bool use_lean_kernel(int batch, int head_dim, int n_kv, int R, int page_size, int split_tokens,
                             int32_t flags) {
-  return head_dim == rows::HD && n_kv == rows::NKV && R <= 16 && page_size >= rows::TILE &&
+  return head_dim == rows::HD && n_kv == rows::NKV && R <= kLeanMaxRows && page_size >= rows::TILE &&
          batch <= rows::kMaxBatch && split_tokens <= 0 && !(flags & (PKV_DECODE_HEADS | PKV_DECODE_FUSED_MERGE));
 }
 
@@ -1862,8 +1933,13 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
     p.ws_ml = p.ws_o + size_t(2) * grid * rows::NKV * R * rows::HD;
     p.two_pass = 1;
     p.lean_grid = grid;
-    decode_lean_kernel<<<grid, 64 * rows::NKV, 0, s>>>(p);
-    combine_lean_kernel<<<dim3(rows::NKV, batch), 64 * R, 0, s>>>(p, grid);
+    switch ((R + 15) / 16) {
+      case 1: decode_lean_kernel<1><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
+      case 2: decode_lean_kernel<2><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
+      case 3: decode_lean_kernel<3><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
+      default: decode_lean_kernel<4><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
+    }
+    combine_lean_kernel<<<dim3(rows::NKV, batch, (R + 15) / 16), 64 * (R < 16 ? R : 16), 0, s>>>(p, grid);
     return check_launch(fn);
   }
 

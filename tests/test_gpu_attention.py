@@ -77,9 +77,10 @@ def test_split_merge_rearms_across_calls_and_matches_two_pass(gpu):
                            split_tokens=256, seed=i, two_pass=two_pass, what=f"rearm{i}")
 
 
-# The balanced kernel (head_dim 128, 4 KV heads, pages >= 32, <= 16 query rows per KV head):
+# The balanced kernel (head_dim 128, 4 KV heads, pages >= 32, <= 64 query rows per KV head):
 # grids from one workgroup (every tile in one range, several 64-tile descriptor windows) to more
-# workgroups than tiles, ranges holding many short sequences, new rows straddling a tile edge.
+# workgroups than tiles, ranges holding many short sequences, new rows straddling a tile edge;
+# 1 to 4 MFMA row tiles per wave (R = 7 .. 63: decode and speculative verify).
 LEAN_CASES = [
     # (batch, ctx, page, n_heads, s_q, grid, append)
     (6, [3000, 17, 4100, 800, 1, 2500], 256, 28, 1, 0, True),
@@ -92,6 +93,14 @@ LEAN_CASES = [
     (5, [10, 20, 30, 40, 50], 256, 28, 1, 64, True),
     (70, [(i * 53) % 900 for i in range(70)], 256, 28, 1, 0, True),
     (70, [(i * 53) % 900 for i in range(70)], 256, 28, 1, 9, True),
+    (3, [517, 2, 90], 256, 28, 5, 0, True),                 # verify R = 35: 3 row tiles
+    (3, [517, 2, 90], 256, 28, 5, 5, True),
+    (6, [3000, 17, 4100, 800, 1, 2500], 256, 28, 4, 7, True),  # R = 28: 2 row tiles
+    (4, [700, 33, 1, 2000], 256, 28, 9, 6, True),           # R = 63: 4 row tiles, appends straddle tiles
+    (40, [(i * 37) % 300 for i in range(40)], 32, 28, 5, 5, True),
+    (2, [61, 700], 256, 16, 8, 3, False),                   # g = 4, R = 32, no append
+    (1, [0], 256, 28, 6, 1, True),                          # empty cache, R = 42
+    (64, [2027 + (i * 97) % 1024 for i in range(64)], 256, 28, 5, 0, True),  # config-5 shape
 ]
 
 
@@ -102,7 +111,8 @@ def test_balanced_decode_kernel(gpu, case):
                    append=append, grid=grid, seed=len(ctx) + grid, what=f"lean{case[:1] + case[2:]}")
 
 
-@pytest.mark.parametrize("case", [DECODE_CASES[1], DECODE_CASES[4], DECODE_CASES[7]], ids=["d1", "d4", "d7"])
+@pytest.mark.parametrize("case", [DECODE_CASES[1], DECODE_CASES[4], DECODE_CASES[5], DECODE_CASES[7]],
+                         ids=["d1", "d4", "d5", "d7"])
 def test_per_head_kernel_on_balanced_shapes(gpu, case):
     # the same shapes through the per-(sequence, head, split) kernel, both merges
     B, ctx, P, n_kv, nh, hd, s_q = case
@@ -123,6 +133,8 @@ def test_decode_without_append_and_non_causal(gpu):
                    append=False, what="noappend")
     _run_and_check(gpu, batch=2, ctx=[77, 400], page_size=256, n_kv=4, n_heads=28, head_dim=128, s_q=3,
                    causal=False, what="noncausal")
+    _run_and_check(gpu, batch=3, ctx=[77, 400, 5], page_size=256, n_kv=4, n_heads=28, head_dim=128, s_q=5,
+                   causal=False, grid=4, what="noncausal-verify")
 
 
 def test_decode_extra_block_table_columns(gpu):
