@@ -802,6 +802,10 @@ constexpr int BUF_BYTES = 2 * TILE_BYTES + Q_BYTES;  // one LDS buffer: K tile |
 // per call, and streaming it past the caches' normal allocation measured ~12% faster for the
 // 7B decode step's 115 MB (18.7 vs 21.1 us per launch for the bare copy loop).
 constexpr int kStreamPolicy = 2;
+// Verify (several query rows per head) reads its tiles with the default policy instead: the
+// sequences of a verify batch usually share a cached prefix, whose pages then stay in the caches
+// for the next sequence (config-5 verify: 78.3 vs 82.0 us per call).
+constexpr int kVerifyPolicy = 0;
 typedef __attribute__((address_space(3))) void lds_void;
 }  // namespace rows
 
@@ -959,7 +963,9 @@ __device__ __forceinline__ bool tile_has_new(const AttnParams& p, const TileDesc
 // cache, so attention sees it without waiting for the append.  When the tile starts a segment
 // (with_q), 4 more copies per wave bring the Q operand rows of head w into the buffer's Q area:
 // row r (clamped to R - 1) at [w][r], LDS chunk l holding global chunk l ^ (r & 15).
-__device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& d, bool with_q, char* buf) {
+template <int POLICY = rows::kStreamPolicy>
+__device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& d, bool with_q, char* buf,
+                                           int I0 = 0, int I1 = rows::TILE / rows::NKV) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t off = int64_t(d.pid < 0 ? 0 : d.pid) * p.page_stride +
@@ -968,7 +974,7 @@ __device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& 
   const char* vg = uniform_ptr(reinterpret_cast<const char*>(p.v_cache + off));
   const bool any_new = tile_has_new(p, d);
 #pragma unroll
-  for (int i = 0; i < rows::TILE / rows::NKV; ++i) {
+  for (int i = I0; i < I1; ++i) {
     const int r = i * rows::NKV + wave;
     const int t = d.T0 + r;
     const uint32_t gc = uint32_t(lane ^ rows::swz(r));
@@ -981,9 +987,9 @@ __device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& 
       ks = reinterpret_cast<const char*>(p.k_new + d.b * p.kn_sb + jn * p.kn_ss + hh * p.kn_sh + w8);
       vs = reinterpret_cast<const char*>(p.v_new + d.b * p.vn_sb + jn * p.vn_ss + hh * p.vn_sh + w8);
     }
-    __builtin_amdgcn_global_load_lds(ks, (rows::lds_void*)(buf + r * rows::ROW_BYTES), 16, 0, rows::kStreamPolicy);
+    __builtin_amdgcn_global_load_lds(ks, (rows::lds_void*)(buf + r * rows::ROW_BYTES), 16, 0, POLICY);
     __builtin_amdgcn_global_load_lds(vs, (rows::lds_void*)(buf + rows::TILE_BYTES + r * rows::ROW_BYTES), 16, 0,
-                                     rows::kStreamPolicy);
+                                     POLICY);
   }
   if (with_q) {
 #pragma unroll
@@ -1103,16 +1109,23 @@ __device__ __forceinline__ void rows_load_q(const AttnParams& p, const TileDesc&
   }
 }
 
+template <int NT>
+__device__ __forceinline__ void compute_tile_prefill(const AttnParams& p, const KVTile<128>& tl, int T0,
+                                                     const bf16x8 (&qf)[NT][4], const int (&lim)[NT], int lim_min,
+                                                     float (&m_run)[NT], float (&l_run)[NT], f32x4 (&acc)[NT][8]);
+
 // NT = 16-row MFMA N tiles per wave: R <= 16 * NT query rows per KV head.  NT = 1 (decode) brings
 // a segment's Q through the LDS buffers with the tile copies; NT > 1 (speculative verify) loads Q
 // into registers at the segment start and rounds P to bf16 once (its MFMA work is NT times
-// decode's, so it gives up the hi + lo split).
+// decode's, so it gives up the hi + lo split).  Verify: 152 us per config-5 call on
+// decode_kernel, 70 us here.
 template <int NT>
 __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p) {
   constexpr int HD = rows::HD;
   constexpr int DPL = HD / 16;
   constexpr bool kQInLds = NT == 1;
   constexpr int BUF = kQInLds ? rows::BUF_BYTES : 2 * rows::TILE_BYTES;
+  constexpr int kPolicy = NT == 1 ? rows::kStreamPolicy : rows::kVerifyPolicy;
   __shared__ __attribute__((aligned(16))) char lds[2 * BUF];
 
   const int lane = threadIdx.x & 63;
@@ -1132,10 +1145,10 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   tile_window(p, st, s, e, win);
   TileDesc dA = tile_desc(win, s);
   TileDesc dB = dA;
-  rows_issue(p, dA, kQInLds, lds);
+  rows_issue<kPolicy>(p, dA, kQInLds, lds);
   if (n > 1) {
     dB = tile_desc(win, s + 1);
-    rows_issue(p, dB, kQInLds && dB.T0 == 0, lds + BUF);
+    rows_issue<kPolicy>(p, dB, kQInLds && dB.T0 == 0, lds + BUF);
   }
 
   bf16x8 qf[NT][HD / 32];
@@ -1201,17 +1214,29 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     rows_read_tile(buf, h, d.T0, d.L, tl);
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
     raw_barrier();                       // nobody reads this buffer any more
-    if (j + 2 < n) {
+    // Tile j + 2's copies go out in two halves, one before and one after tile j's compute: this
+    // wave's copy issue stalls while earlier copies drain, and the split lets that stall overlap
+    // the compute (7B decode 31.0 -> 30.7 us, config-5 verify 77.8 -> 74.5 us per call, against
+    // issuing all of them before the compute).
+    TileDesc d2 = dB;
+    const bool next2 = j + 2 < n;
+    if (next2) {
       const int x2 = s + j + 2;
       if (x2 - win.x0 >= 64) tile_window(p, st, x2, e, win);
-      const TileDesc d2 = tile_desc(win, x2);
-      rows_issue(p, d2, kQInLds && d2.T0 == 0, buf);
-      dA = dB;
-      dB = d2;
-    } else {
-      dA = dB;
+      d2 = tile_desc(win, x2);
+      rows_issue<kPolicy>(p, d2, false, buf, 0, 4);
     }
-    if (d.T0 < d.L) compute_tile<HD, NT, NT == 1>(p, tl, d.T0, qf, lim, lim_min, m_run, l_run, acc);
+    dA = dB;
+    dB = d2;
+    if (d.T0 < d.L) {
+      // verify: the prefill kernel's ILP-ordered tile update (all QK products, then the softmax
+      // of every N tile, then every PV product)
+      if constexpr (NT > 1)
+        compute_tile_prefill<NT>(p, tl, d.T0, qf, lim, lim_min, m_run, l_run, acc);
+      else
+        compute_tile<HD, NT, true>(p, tl, d.T0, qf, lim, lim_min, m_run, l_run, acc);
+    }
+    if (next2) rows_issue<kPolicy>(p, d2, kQInLds && d2.T0 == 0, buf, 4, 8);
 
     stores_prev2 = stores_prev;
     stores_prev = 0;
@@ -1254,10 +1279,10 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
           float* dst = p.ws_o + row * HD + 4 * DPL * lq;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            *reinterpret_cast<f32x4*>(dst + DPL * r) =
-                f32x4{acc[nt][0][r], acc[nt][1][r], acc[nt][2][r], acc[nt][3][r]};
-            *reinterpret_cast<f32x4*>(dst + DPL * r + 4) =
-                f32x4{acc[nt][4][r], acc[nt][5][r], acc[nt][6][r], acc[nt][7][r]};
+            const f32x4 lo = f32x4{acc[nt][0][r], acc[nt][1][r], acc[nt][2][r], acc[nt][3][r]};
+            const f32x4 hi = f32x4{acc[nt][4][r], acc[nt][5][r], acc[nt][6][r], acc[nt][7][r]};
+            *reinterpret_cast<f32x4*>(dst + DPL * r) = lo;
+            *reinterpret_cast<f32x4*>(dst + DPL * r + 4) = hi;
           }
           if (lq == 0) *reinterpret_cast<f32x2*>(p.ws_ml + row * 2) = f32x2{m_run[nt], lsum[nt]};
         }
