@@ -47,8 +47,8 @@ extern "C" {
 #define PKV_STATUS_BAD_PAGE 1
 
 /* pkv_decode_attn flags (0 = the library's choice of kernel and merge) */
-#define PKV_DECODE_TWO_PASS 1    /* per-head kernel: merge split-K partials in a second launch */
-#define PKV_DECODE_FUSED_MERGE 2 /* per-head kernel, partials merged by the last workgroup to finish */
+#define PKV_DECODE_TWO_PASS 1    /* merge split-K partials in a second launch */
+#define PKV_DECODE_FUSED_MERGE 2 /* merge split-K partials in the attention launch (last part to finish) */
 #define PKV_DECODE_HEADS 4       /* use the per-head kernel where the balanced one would run */
 #define PKV_DECODE_GRID(n) ((int32_t)(n) << 8) /* balanced kernel on n (1..65535) workgroups, not one per CU */
 
@@ -97,11 +97,12 @@ size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, i
  * head_dim] with the given strides.  A query row with no visible key gets zeros.
  * Two kernels serve the call.  Where head_dim = 128, n_kv = 4, page_size >= 32,
  * batch <= 256 (the Qwen2.5-7B decode and verify shapes), split_tokens = 0 and
- * neither PKV_DECODE_HEADS nor PKV_DECODE_FUSED_MERGE is set, a balanced kernel gives every
- * workgroup an equal share of all sequences' 32-token KV tiles and a second launch merges the
- * sequences that straddle shares.  Otherwise a per-(sequence, KV head, split) kernel reduces
- * split_tokens keys (a multiple of 32; 0 = 512) per workgroup and merges the splits inside the
- * launch (PKV_DECODE_TWO_PASS: in a second launch).  Results agree up to fp32 rounding order.
+ * PKV_DECODE_HEADS is not set, a balanced kernel gives every workgroup an equal share of all
+ * sequences' 32-token KV tiles; the sequences that straddle shares are merged by a second launch
+ * (PKV_DECODE_FUSED_MERGE: inside the launch, by the last share of a sequence to finish).
+ * Otherwise a per-(sequence, KV head, split) kernel reduces split_tokens keys (a multiple of 32;
+ * 0 = 512) per workgroup and merges the splits inside the launch (PKV_DECODE_TWO_PASS: in a
+ * second launch).  Results agree up to rounding (fp32 order, fp16 split-K partials).
  * workspace must hold pkv_decode_workspace_bytes() bytes and be
  * zero-filled before its first use; every call leaves it in that state again (its first 64 KiB
  * hold per-(sequence, KV head) arrival counters, so batch * n_kv <= 16384 when a sequence can

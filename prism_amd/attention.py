@@ -186,9 +186,10 @@ def flash_attn_with_kvcache(
     Arguments Prism never passes (rotary_*, cache_batch_idx, cache_leftpad, window_size,
     softcap, alibi_slopes, return_softmax_lse) must keep their defaults.  ``num_splits`` > 0
     fixes the number of KV splits per sequence; ``split_tokens`` > 0 (a multiple of 32) fixes
-    the split length directly (both select the per-head kernel); ``two_pass`` True merges that
-    kernel's split-K partials in a second launch, False inside the attention launch, None lets the
-    library choose.  ``kernel="heads"`` forces the per-head kernel where the balanced one would
+    the split length directly (both select the per-head kernel); ``two_pass`` True merges the
+    split-K partials in a second launch, False inside the attention launch (by the last workgroup
+    to finish its part of a sequence), None lets the library choose (a second launch for the
+    balanced kernel, in-launch for the per-head kernel).  ``kernel="heads"`` forces the per-head kernel where the balanced one would
     run; ``grid`` > 0 runs the balanced kernel on that many workgroups instead of one per CU.
     """
     if rotary_cos is not None or rotary_sin is not None or cache_batch_idx is not None \

@@ -1114,11 +1114,190 @@ __device__ __forceinline__ void compute_tile_prefill(const AttnParams& p, const 
                                                      const bf16x8 (&qf)[NT][4], const int (&lim)[NT], int lim_min,
                                                      float (&m_run)[NT], float (&l_run)[NT], f32x4 (&acc)[NT][8]);
 
-// NT = 16-row MFMA N tiles per wave: R <= 16 * NT query rows per KV head.  NT = 1 (decode) brings
-// a segment's Q through the LDS buffers with the tile copies; NT > 1 (speculative verify) loads Q
-// into registers at the segment start and rounds P to bf16 once (its MFMA work is NT times
-// decode's, so it gives up the hi + lo split).  Verify: 152 us per config-5 call on
-// decode_kernel, 70 us here.
+// ---- split-K partials of decode_lean_kernel, merged inside the launch ----
+// Partials are written and read through a buffer resource on the workspace with the sc1 cache
+// policy: device-coherent accesses (what agent-scope atomics compile to on gfx950), so a
+// workgroup on one XCD reads what another XCD wrote without any L2-wide writeback or
+// invalidate.  Byte offsets are relative to ws_o; the (m, l) pairs follow at ws_ml.
+constexpr int kCoherent = 16;  // cache-policy bit sc1
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(const AttnParams& p) {
+  return __builtin_amdgcn_make_buffer_rsrc(p.ws_o, 0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ void ws_st16(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, int(off), 0, kCoherent);
+}
+__device__ __forceinline__ void ws_st8(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, int(off), 0, kCoherent);
+}
+__device__ __forceinline__ f32x4 ws_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, int(off), 0, kCoherent));
+}
+__device__ __forceinline__ f32x2 ws_ld8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, int(off), 0, kCoherent));
+}
+
+// Stores of one (row, lane) share of an fp16 partial and its log-sum-exp with cache policy POL:
+// device-coherent (kCoherent) when the merge runs inside the launch, plain for the two-pass merge.
+template <int POL>
+__device__ __forceinline__ void ws_store_partial(__amdgpu_buffer_rsrc_t rs, uint32_t o_off, const u32x4 (&ov)[4],
+                                                 bool with_lse, uint32_t lse_off, float lse) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) __builtin_amdgcn_raw_buffer_store_b128(ov[r], rs, int(o_off + 16u * r), 0, POL);
+  if (with_lse) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, lse), rs, int(lse_off), 0, POL);
+}
+
+// Parts of sequence b in a balanced launch: the ranges w0..w1 its tiles fall in (per tiles each)
+// and the workspace slot of part 0 (range w0 holds b in its first segment only when b starts at
+// w0's first tile; every later part is its range's first segment, slot 2w).
+struct SeqParts {
+  int np, w0, slot0;
+};
+
+__device__ __forceinline__ SeqParts seq_parts(const SeqTable& st, int b, int per) {
+  int first = 0, L = 0;
+#pragma unroll
+  for (int q = 0; q < rows::kChunks; ++q) {
+    if (q == (b >> 6)) {
+      first = __builtin_amdgcn_readlane(st.first[q], b & 63);
+      L = __builtin_amdgcn_readlane(st.L[q], b & 63);
+    }
+  }
+  SeqParts sp;
+  sp.w0 = first / per;
+  sp.np = (first + tiles_of(L) - 1) / per - sp.w0 + 1;
+  sp.slot0 = 2 * sp.w0 + (first != sp.w0 * per ? 1 : 0);
+  return sp;
+}
+
+// A split-K partial of (workspace slot, KV head): per query row, O / l as fp16 (16 B per 8
+// head-dim elements; O / l is a convex combination of V rows, so fp16's range and 2^-11 rounding
+// are ample next to the bf16 output) and its log-sum-exp lse = m + log2(l) in fp32 (-inf when
+// the row saw no key).  O of row r: byte (((slot * 4 + h) * R + r) * head_dim) * 2 from ws_o;
+// lse: float ((slot * 4 + h) * R + r) from ws_ml.
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));  // RNE
+}
+__device__ __forceinline__ void unpack_f16x8(const u32x4 v, float (&f)[8]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const _Float16 lo = __builtin_bit_cast(_Float16, uint16_t(v[k] & 0xffffu));
+    const _Float16 hi = __builtin_bit_cast(_Float16, uint16_t(v[k] >> 16));
+    f[2 * k] = float(lo);
+    f[2 * k + 1] = float(hi);
+  }
+}
+
+// Log-sum-exp merge of the np partials of (b, KV head h) into the bf16 output, by one wave.
+// Chunk i = 64c + lane of a part's R x head_dim fp16 block (16 B; row i / 16, head-dim
+// 8 (i % 16)) belongs to lane `lane`; lane r < R keeps row r's running max and weight sum.  All
+// loads of a batch of KB parts (lse and O) are issued before any is used, and the parts'
+// weights reach the chunks through this wave's LDS scratch `wl` ((KB + 2) x 64 floats).
+template <int NC, int KB>
+__device__ __forceinline__ void merge_parts(const AttnParams& p, __amdgpu_buffer_rsrc_t rs, int b, int h,
+                                            const SeqParts& sp, float* wl) {
+  constexpr int HD = rows::HD;
+  const int lane = threadIdx.x & 63;
+  const int R = p.R;
+  const int nch = R * (HD / 8);
+  const uint32_t lse0 = uint32_t(p.ws_ml - p.ws_o) * 4u;
+  float acc[NC][8];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[c][e] = 0.f;
+  float M = -INFINITY, S = 0.f;
+  for (int u0 = 0; u0 < sp.np; u0 += KB) {
+    const int nb = min(KB, sp.np - u0);
+    // lane k: first row of part u0 + k (its slot's block for head h)
+    const int part = u0 + min(lane, nb - 1);
+    const int rb_lane = ((part == 0 ? sp.slot0 : 2 * (sp.w0 + part)) * rows::NKV + h) * R;
+    float lse[KB];
+    u32x4 x[KB][NC];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+      lse[k] = -INFINITY;
+      if (k < nb) {
+        const uint32_t rb = uint32_t(__builtin_amdgcn_readlane(rb_lane, k));
+        if (lane < R)
+          lse[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, int(lse0 + lane * 4u), int(rb * 4u),
+                                                                                  kCoherent));
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int i = 64 * c + lane;
+          x[k][c] = i < nch ? __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * i, int(rb * (HD * 2)), kCoherent)
+                            : u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+    }
+    float Mn = M;
+#pragma unroll
+    for (int k = 0; k < KB; ++k) Mn = fmaxf(Mn, lse[k]);
+    const float Mu = Mn == -INFINITY ? 0.f : Mn;
+    const float resc = fast_exp2(M - Mu);
+    S *= resc;
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+      const float wk = k < nb ? fast_exp2(lse[k] - Mu) : 0.f;
+      S += wk;
+      wl[64 * k + lane] = wk;
+    }
+    wl[64 * KB + lane] = resc;
+    M = Mn;
+    // the weights were written by this wave's own lanes: its LDS operations complete in order
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int i = 64 * c + lane;
+      if (i < nch) {
+        const int row = i >> 4;
+        const float rs_ = wl[64 * KB + row];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[c][e] *= rs_;
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+          if (k < nb) {
+            const float wk = wl[64 * k + row];
+            float f[8];
+            unpack_f16x8(x[k][c], f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[c][e] += wk * f[e];
+          }
+        }
+      }
+    }
+  }
+  wl[64 * (KB + 1) + lane] = S > 0.f ? 1.f / S : 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int i = 64 * c + lane;
+    if (i < nch) {
+      const int row = i >> 4;
+      const float inv = wl[64 * (KB + 1) + row];
+      const int j = row / p.g;
+      const int hq = row - j * p.g;
+      u32x4 ov;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[c][2 * k] * inv, acc[c][2 * k + 1] * inv);
+      st16(p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + 8 * (i & 15), ov);
+    }
+  }
+}
+
+// merge_parts for the row count of the launch: all loads of up to 32 parts (R <= 8) in flight.
+template <int NT>
+__device__ __forceinline__ void merge_parts_for(const AttnParams& p, __amdgpu_buffer_rsrc_t rs, int b, int h,
+                                                const SeqParts& sp, float* wl) {
+  if constexpr (NT == 1) {
+    if (p.R <= 8)
+      merge_parts<2, 32>(p, rs, b, h, sp, wl);
+    else
+      merge_parts<4, 8>(p, rs, b, h, sp, wl);
+  } else {
+    merge_parts<4 * NT, 8 / NT>(p, rs, b, h, sp, wl);
+  }
+}
+
 template <int NT>
 __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p) {
   constexpr int HD = rows::HD;
@@ -1167,6 +1346,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   int seg_j0 = 0;  // range index of the current segment's first tile
   int seg_T0 = 0;  // its first token
   int stores_prev = 0, stores_prev2 = 0;  // epilogue stores of iterations j-1 and j-2 (lower bounds)
+  int pub_first = -1, pub_last = -1;  // sequences of the partials in slots 2w and 2w + 1
   for (int j = 0; j < n; ++j) {
     const TileDesc d = dA;
     char* buf = lds + (j & 1) * BUF;
@@ -1242,9 +1422,9 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     stores_prev = 0;
     if (j + 1 < n && d.T0 + rows::TILE < d.L) continue;  // the segment goes on
     // ---- segment epilogue: wave h owns head h's rows li + 16 nt < R (per N tile 4 stores, or
-    // 8 + 1 for a partial; every N tile has a real row) ----
+    // 4 + 1 for a partial; every N tile has a real row) ----
     const bool whole = seg_T0 == 0 && d.T0 + rows::TILE >= d.L;
-    stores_prev = (whole ? 4 : 8) * NT;
+    stores_prev = (whole ? 4 : 5) * NT;
     float lsum[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) lsum[nt] = sum_over_quads(l_run[nt]);
@@ -1268,26 +1448,64 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
         }
       }
     } else {
-      // part of a sequence shared with a neighbouring range: unnormalised partial, merged by the
-      // combine launch (the kernel boundary orders these plain stores before its loads)
+      // part of a sequence shared with a neighbouring range: unnormalised partial (device-
+      // coherent stores), merged at the end of the launch by the last range to finish its part,
+      // or by the combine launch (two-pass)
       const int slot = 2 * int(blockIdx.x) + (seg_j0 == 0 ? 0 : 1);
+      if (seg_j0 == 0)
+        pub_first = d.b;
+      else
+        pub_last = d.b;
+      const uint32_t lse0 = uint32_t(p.ws_ml - p.ws_o) * 4u;
+      const __amdgpu_buffer_rsrc_t rs = ws_rsrc(p);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int rr = li + 16 * nt;
         if (rr < p.R) {
-          const int64_t row = (int64_t(slot) * rows::NKV + h) * p.R + rr;
-          float* dst = p.ws_o + row * HD + 4 * DPL * lq;
+          const uint32_t row = uint32_t((slot * rows::NKV + h) * p.R + rr);
+          const float inv = lsum[nt] > 0.f ? 1.f / lsum[nt] : 0.f;
+          u32x4 ov[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const f32x4 lo = f32x4{acc[nt][0][r], acc[nt][1][r], acc[nt][2][r], acc[nt][3][r]};
-            const f32x4 hi = f32x4{acc[nt][4][r], acc[nt][5][r], acc[nt][6][r], acc[nt][7][r]};
-            *reinterpret_cast<f32x4*>(dst + DPL * r) = lo;
-            *reinterpret_cast<f32x4*>(dst + DPL * r + 4) = hi;
-          }
-          if (lq == 0) *reinterpret_cast<f32x2*>(p.ws_ml + row * 2) = f32x2{m_run[nt], lsum[nt]};
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) ov[r][k] = pack_f16x2(acc[nt][2 * k][r] * inv, acc[nt][2 * k + 1][r] * inv);
+          const float lse = lsum[nt] > 0.f ? m_run[nt] + __builtin_amdgcn_logf(lsum[nt]) : -INFINITY;
+          const uint32_t o_off = (row * HD + 4 * DPL * lq) * 2u;
+          if (p.two_pass)
+            ws_store_partial<0>(rs, o_off, ov, lq == 0, lse0 + row * 4u, lse);
+          else
+            ws_store_partial<kCoherent>(rs, o_off, ov, lq == 0, lse0 + row * 4u, lse);
         }
       }
     }
+  }
+  if (p.two_pass || (pub_first < 0 && pub_last < 0)) return;
+  // In-launch merge.  Once this wave's partial stores have completed, count its arrival at each
+  // sequence it wrote a part of; the wave that brings a (sequence, head) counter to its part
+  // count merges every part and re-arms the counter for the next call.  Nobody waits.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the partial stores are device-visible
+  const __amdgpu_buffer_rsrc_t rs = ws_rsrc(p);
+  float* wl = reinterpret_cast<float*>(lds) + h * 2304;  // tile buffers are free after the loop
+  // both arrivals in flight together, then the merges this wave completes
+  int prev0 = 0, prev1 = 0;
+  if (lane == 0) {
+    if (pub_first >= 0)
+      prev0 = __hip_atomic_fetch_add(p.ws_cnt + pub_first * rows::NKV + h, 1, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+    if (pub_last >= 0)
+      prev1 = __hip_atomic_fetch_add(p.ws_cnt + pub_last * rows::NKV + h, 1, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+  }
+  prev0 = __builtin_amdgcn_readfirstlane(prev0);
+  prev1 = __builtin_amdgcn_readfirstlane(prev1);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int b = k == 0 ? pub_first : pub_last;
+    if (b < 0) continue;
+    const SeqParts sp = seq_parts(st, b, per);
+    if ((k == 0 ? prev0 : prev1) != sp.np - 1) continue;
+    if (lane == 0) __hip_atomic_store(p.ws_cnt + b * rows::NKV + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    merge_parts_for<NT>(p, rs, b, h, sp, wl);
   }
 }
 
@@ -1308,11 +1526,12 @@ __device__ __forceinline__ float wave_sum(float v) {
   return sum_over_quads(v);
 }
 
-// Merge of the partials a decode_lean_kernel launch of `grid` workgroups left in the workspace.
-// Workgroup (KV head, sequence, group of 16 query rows), one wave per query row; only sequences
-// whose tiles span more than one range have partials.  Lane u holds part u's (m, l) of the row; for the output lane l owns
-// head-dim elements 2l and 2l + 1 and reads them from every part, all loads of a batch of 32
-// parts in flight at once; the parts' weights reach every lane by v_readlane.  No LDS, no barrier.
+// Two-pass merge (PKV_DECODE_TWO_PASS) of the partials a decode_lean_kernel launch of `grid`
+// workgroups left in the workspace.  Workgroup (KV head, sequence, group of 16 query rows), one
+// wave per query row; only sequences whose tiles span more than one range have partials.  Lane
+// u holds part u's log-sum-exp; lane l owns head-dim elements 2l and 2l + 1 and reads them from
+// every part, all loads of a batch of 32 parts in flight at once; the parts' weights reach every
+// lane by v_readlane.  No LDS, no barrier.
 constexpr int kLeanMergeBatch = 32;
 
 __global__ __launch_bounds__(1024) void combine_lean_kernel(const AttnParams p, int grid) {
@@ -1344,34 +1563,36 @@ __global__ __launch_bounds__(1024) void combine_lean_kernel(const AttnParams p, 
     const int slot = part == 0 ? slot0 : 2 * (w0 + part);
     return (int64_t(slot) * rows::NKV + h) * p.R + r;
   };
-  float M_run = -INFINITY, l_run = 0.f;
+  const uint32_t* o16 = reinterpret_cast<const uint32_t*>(p.ws_o);  // fp16 pairs
+  float M_run = -INFINITY, S_run = 0.f;
   f32x2 o = {0.f, 0.f};
   for (int u0 = 0; u0 < np; u0 += kLeanMergeBatch) {
     const int nb = min(kLeanMergeBatch, np - u0);
-    f32x2 x[kLeanMergeBatch];
+    uint32_t x[kLeanMergeBatch];
 #pragma unroll
     for (int k = 0; k < kLeanMergeBatch; ++k) {
-      x[k] = f32x2{0.f, 0.f};
-      if (k < nb) x[k] = *reinterpret_cast<const f32x2*>(p.ws_o + row_of(u0 + k) * HD + 2 * lane);
+      x[k] = 0u;
+      if (k < nb) x[k] = o16[row_of(u0 + k) * (HD / 2) + lane];
     }
-    float m = -INFINITY, l = 0.f;
-    if (lane < nb) {
-      const f32x2 ml = *reinterpret_cast<const f32x2*>(p.ws_ml + row_of(u0 + lane) * 2);
-      m = ml[0];
-      l = ml[1];
-    }
-    const float M_new = fmaxf(M_run, wave_max(m));
+    const float lse = lane < nb ? p.ws_ml[row_of(u0 + lane)] : -INFINITY;
+    const float M_new = fmaxf(M_run, wave_max(lse));
     const float M_use = (M_new == -INFINITY) ? 0.f : M_new;
-    const float w = fast_exp2(m - M_use);
+    const float w = fast_exp2(lse - M_use);
     const float resc = fast_exp2(M_run - M_use);
-    l_run = l_run * resc + wave_sum(w * l);
+    S_run = S_run * resc + wave_sum(w);
     M_run = M_new;
     o *= resc;
 #pragma unroll
-    for (int k = 0; k < kLeanMergeBatch; ++k)
-      if (k < nb) o += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), k)) * x[k];
+    for (int k = 0; k < kLeanMergeBatch; ++k) {
+      if (k < nb) {
+        const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), k));
+        const _Float16 lo = __builtin_bit_cast(_Float16, uint16_t(x[k] & 0xffffu));
+        const _Float16 hi = __builtin_bit_cast(_Float16, uint16_t(x[k] >> 16));
+        o += wk * f32x2{float(lo), float(hi)};
+      }
+    }
   }
-  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+  const float inv = S_run > 0.f ? 1.f / S_run : 0.f;
   const int j = r / p.g;
   const int hq = r - j * p.g;
   *reinterpret_cast<uint32_t*>(p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + 2 * lane) =
@@ -1759,7 +1980,7 @@ constexpr int kLeanMaxRows = PKV_LEAN_MAX_ROWS;
 static bool use_lean_kernel(int batch, int head_dim, int n_kv, int R, int page_size, int split_tokens,
                             int32_t flags) {
   return head_dim == rows::HD && n_kv == rows::NKV && R <= kLeanMaxRows && page_size >= rows::TILE &&
-         batch <= rows::kMaxBatch && split_tokens <= 0 && !(flags & (PKV_DECODE_HEADS | PKV_DECODE_FUSED_MERGE));
+         batch <= rows::kMaxBatch && split_tokens <= 0 && !(flags & PKV_DECODE_HEADS);
 }
 
 // Workgroups of a decode_lean_kernel launch: PKV_DECODE_GRID(n) of the flags, else one per CU.
@@ -1948,15 +2169,21 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
   p.batch = batch;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (lean) {
-    // balanced row-streaming kernel; its partials are always merged by a second launch
+    // balanced row-streaming kernel; partials merged by a second launch, or inside the launch
+    // with PKV_DECODE_FUSED_MERGE (slower on the 7B decode step: the merge of a long sequence's
+    // ~27 parts by its last range costs more than the second launch)
     const int grid = lean_grid(flags);
     const size_t need = ws_bytes_lean(grid, R);
+    if (need - kCounterBytes >= (size_t(1) << 31))
+      return fail(PKV_EINVAL, "%s: %d workgroups need a %zu-byte workspace (partials must stay under 2 GiB)",
+                  fn, grid, need);
     if (!workspace || workspace_bytes < need)
       return fail(PKV_ENOSPC, "%s: workspace %zu bytes < %zu needed", fn, workspace_bytes, need);
     if (!aligned16(workspace)) return fail(PKV_EINVAL, "%s: workspace not 16-byte aligned", fn);
+    p.ws_cnt = static_cast<int32_t*>(workspace);
     p.ws_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
     p.ws_ml = p.ws_o + size_t(2) * grid * rows::NKV * R * rows::HD;
-    p.two_pass = 1;
+    p.two_pass = merge == PKV_DECODE_FUSED_MERGE ? 0 : 1;
     p.lean_grid = grid;
     switch ((R + 15) / 16) {
       case 1: decode_lean_kernel<1><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
@@ -1964,7 +2191,8 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
       case 3: decode_lean_kernel<3><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
       default: decode_lean_kernel<4><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
     }
-    combine_lean_kernel<<<dim3(rows::NKV, batch, (R + 15) / 16), 64 * (R < 16 ? R : 16), 0, s>>>(p, grid);
+    if (p.two_pass)
+      combine_lean_kernel<<<dim3(rows::NKV, batch, (R + 15) / 16), 64 * (R < 16 ? R : 16), 0, s>>>(p, grid);
     return check_launch(fn);
   }
 

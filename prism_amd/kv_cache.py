@@ -132,10 +132,13 @@ class FlashAttnKVCache:
         self.seq_owner[seq_id] = owner
 
     def fork_sequence(self, src_seq_id: int, dst_seq_id: int, owner: str | None = None) -> None:
-        """dst shares every page of src (no copy); the first write into a shared page copies it."""
+        """dst shares every page of src (no copy); the first write into a shared page copies it.
+        Forking a sequence into itself changes nothing."""
+        pages = list(self.seq_pages[src_seq_id])
+        if dst_seq_id == src_seq_id:
+            return
         if dst_seq_id in self.seq_pages:
             self.free_sequence(dst_seq_id)
-        pages = list(self.seq_pages[src_seq_id])
         for p in pages:
             self._hold(p)
         self.seq_pages[dst_seq_id] = pages

@@ -104,11 +104,25 @@ LEAN_CASES = [
 ]
 
 
+@pytest.mark.parametrize("merge", ["two-pass", "in-launch"])
 @pytest.mark.parametrize("case", LEAN_CASES, ids=[f"l{i}" for i in range(len(LEAN_CASES))])
-def test_balanced_decode_kernel(gpu, case):
+def test_balanced_decode_kernel(gpu, case, merge):
     B, ctx, P, nh, s_q, grid, append = case
     _run_and_check(gpu, batch=B, ctx=ctx, page_size=P, n_kv=4, n_heads=nh, head_dim=128, s_q=s_q,
-                   append=append, grid=grid, seed=len(ctx) + grid, what=f"lean{case[:1] + case[2:]}")
+                   append=append, grid=grid, two_pass=merge == "two-pass", seed=len(ctx) + grid,
+                   what=f"lean{case[:1] + case[2:]}-{merge}")
+
+
+def test_balanced_in_launch_merge_rearms_across_calls(gpu):
+    # the balanced kernel's per-(sequence, head) arrival counters must be back at zero after every
+    # call: consecutive calls of different shapes and grids share one workspace, with sequences
+    # split into up to ~20 parts, and each result must match the oracle (and so the two-pass merge)
+    shapes = [(6, [3000, 17, 4100, 800, 1, 2500], 7), (2, [5000, 40], 16), (1, [33], 3),
+              (40, [(i * 37) % 300 for i in range(40)], 5), (3, [9000, 600, 1], 21)]
+    for i, (B, ctx, grid) in enumerate(shapes * 2):
+        for two_pass in (False, True):
+            _run_and_check(gpu, batch=B, ctx=ctx, page_size=256, n_kv=4, n_heads=28, head_dim=128, s_q=1,
+                           grid=grid, seed=i, two_pass=two_pass, what=f"lean-rearm{i}")
 
 
 @pytest.mark.parametrize("case", [DECODE_CASES[1], DECODE_CASES[4], DECODE_CASES[5], DECODE_CASES[7]],

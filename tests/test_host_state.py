@@ -139,6 +139,18 @@ def test_write_that_starts_on_a_page_boundary_copies_nothing(copies):
     _check_invariants(kv)
 
 
+def test_fork_into_itself_changes_nothing(copies):
+    kv = _kv(pages=8, P=4)
+    kv.new_sequence(0)
+    kv._ensure_capacity(0, 6)
+    kv.seq_len[0] = 6
+    pages, holders = list(kv.seq_pages[0]), dict(kv._holders)
+    kv.fork_sequence(0, 0)
+    assert kv.seq_pages[0] == pages and kv._holders == holders and kv.seq_len[0] == 6
+    assert copies == []
+    _check_invariants(kv)
+
+
 def test_migrate_and_compact_bookkeeping(copies):
     kv = _kv(pages=12, P=4)
     pc = PrefixCache(kv, page_size=4)
