@@ -1115,28 +1115,15 @@ __device__ __forceinline__ void compute_tile_prefill(const AttnParams& p, const 
                                                      float (&m_run)[NT], float (&l_run)[NT], f32x4 (&acc)[NT][8]);
 
 // ---- split-K partials of decode_lean_kernel, merged inside the launch ----
-// Partials are written and read through a buffer resource on the workspace with the sc1 cache
-// policy: device-coherent accesses (what agent-scope atomics compile to on gfx950), so a
-// workgroup on one XCD reads what another XCD wrote without any L2-wide writeback or
-// invalidate.  Byte offsets are relative to ws_o; the (m, l) pairs follow at ws_ml.
+// For the in-launch merge, partials are written and read with the sc1 cache policy:
+// device-coherent accesses (what agent-scope atomics compile to on gfx950), so a workgroup on one
+// XCD reads what another XCD wrote without any L2-wide writeback or invalidate.  Stores go
+// through a buffer resource on the workspace (byte offsets from ws_o).
 constexpr int kCoherent = 16;  // cache-policy bit sc1
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(const AttnParams& p) {
   return __builtin_amdgcn_make_buffer_rsrc(p.ws_o, 0, 0x7fffffff, 0x00020000);
 }
-__device__ __forceinline__ void ws_st16(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, int(off), 0, kCoherent);
-}
-__device__ __forceinline__ void ws_st8(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x2 v) {
-  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, int(off), 0, kCoherent);
-}
-__device__ __forceinline__ f32x4 ws_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, int(off), 0, kCoherent));
-}
-__device__ __forceinline__ f32x2 ws_ld8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, int(off), 0, kCoherent));
-}
-
 // Stores of one (row, lane) share of an fp16 partial and its log-sum-exp with cache policy POL:
 // device-coherent (kCoherent) when the merge runs inside the launch, plain for the two-pass merge.
 template <int POL>
@@ -1190,18 +1177,26 @@ __device__ __forceinline__ void unpack_f16x8(const u32x4 v, float (&f)[8]) {
 }
 
 // Log-sum-exp merge of the np partials of (b, KV head h) into the bf16 output, by one wave.
-// Chunk i = 64c + lane of a part's R x head_dim fp16 block (16 B; row i / 16, head-dim
-// 8 (i % 16)) belongs to lane `lane`; lane r < R keeps row r's running max and weight sum.  All
-// loads of a batch of KB parts (lse and O) are issued before any is used, and the parts'
-// weights reach the chunks through this wave's LDS scratch `wl` ((KB + 2) x 64 floats).
-template <int NC, int KB>
-__device__ __forceinline__ void merge_parts(const AttnParams& p, __amdgpu_buffer_rsrc_t rs, int b, int h,
-                                            const SeqParts& sp, float* wl) {
+// The code stays small on purpose: it runs once per launch, from a cold instruction cache, so a
+// fully unrolled merge spends microseconds fetching instructions.  Parts come into this wave's
+// LDS area by global->LDS DMA issued from a loop (no register staging, every copy of a batch in
+// flight at once); lane r < R then keeps row r's running max and weight sum, and lane l
+// accumulates float-16 chunks i = 64c + l (row i / 16, head-dim 8 (i % 16)) over the parts.
+// Area layout: [0, 512) per-row rescale and 1 / sum | KB part blocks of R x head_dim fp16 | their
+// log-sum-exps, overwritten by the weights.
+template <int NC>
+__device__ __forceinline__ void merge_parts(const AttnParams& p, int b, int h, const SeqParts& sp, char* area,
+                                            int area_bytes) {
   constexpr int HD = rows::HD;
   const int lane = threadIdx.x & 63;
   const int R = p.R;
+  const int part_bytes = R * HD * 2;
   const int nch = R * (HD / 8);
-  const uint32_t lse0 = uint32_t(p.ws_ml - p.ws_o) * 4u;
+  float* stat = reinterpret_cast<float*>(area);
+  char* oarea = area + 512;
+  const int KB = min(32, (area_bytes - 512) / (part_bytes + 4 * R));
+  float* lsea = reinterpret_cast<float*>(oarea + KB * part_bytes);
+  const char* ws_o = reinterpret_cast<const char*>(p.ws_o);
   float acc[NC][8];
 #pragma unroll
   for (int c = 0; c < NC; ++c)
@@ -1210,70 +1205,64 @@ __device__ __forceinline__ void merge_parts(const AttnParams& p, __amdgpu_buffer
   float M = -INFINITY, S = 0.f;
   for (int u0 = 0; u0 < sp.np; u0 += KB) {
     const int nb = min(KB, sp.np - u0);
-    // lane k: first row of part u0 + k (its slot's block for head h)
-    const int part = u0 + min(lane, nb - 1);
-    const int rb_lane = ((part == 0 ? sp.slot0 : 2 * (sp.w0 + part)) * rows::NKV + h) * R;
-    float lse[KB];
-    u32x4 x[KB][NC];
-#pragma unroll
-    for (int k = 0; k < KB; ++k) {
-      lse[k] = -INFINITY;
-      if (k < nb) {
-        const uint32_t rb = uint32_t(__builtin_amdgcn_readlane(rb_lane, k));
-        if (lane < R)
-          lse[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, int(lse0 + lane * 4u), int(rb * 4u),
-                                                                                  kCoherent));
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const int i = 64 * c + lane;
-          x[k][c] = i < nch ? __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * i, int(rb * (HD * 2)), kCoherent)
-                            : u32x4{0u, 0u, 0u, 0u};
-        }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the previous batch is no longer read
+#pragma unroll 1
+    for (int k = 0; k < nb; ++k) {
+      const int part = u0 + k;
+      const int rb = ((part == 0 ? sp.slot0 : 2 * (sp.w0 + part)) * rows::NKV + h) * R;
+      const char* src = ws_o + int64_t(rb) * (HD * 2);
+#pragma unroll 1
+      for (int q = 0; q * 1024 < part_bytes; ++q)
+        if (q * 1024 + 16 * lane < part_bytes)
+          __builtin_amdgcn_global_load_lds(src + q * 1024 + 16 * lane, (rows::lds_void*)(oarea + k * part_bytes + q * 1024),
+                                           16, 0, kCoherent);
+      if (lane < R)
+        __builtin_amdgcn_global_load_lds(p.ws_ml + rb + lane, (rows::lds_void*)(lsea + k * R), 4, 0, kCoherent);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the batch is in LDS
+    if (lane < R) {
+      float Mn = M;
+#pragma unroll 1
+      for (int k = 0; k < nb; ++k) Mn = fmaxf(Mn, lsea[k * R + lane]);
+      const float Mu = Mn == -INFINITY ? 0.f : Mn;
+      const float resc = fast_exp2(M - Mu);
+      S *= resc;
+#pragma unroll 1
+      for (int k = 0; k < nb; ++k) {
+        const float w = fast_exp2(lsea[k * R + lane] - Mu);
+        S += w;
+        lsea[k * R + lane] = w;
       }
+      stat[lane] = resc;
+      M = Mn;
     }
-    float Mn = M;
-#pragma unroll
-    for (int k = 0; k < KB; ++k) Mn = fmaxf(Mn, lse[k]);
-    const float Mu = Mn == -INFINITY ? 0.f : Mn;
-    const float resc = fast_exp2(M - Mu);
-    S *= resc;
-#pragma unroll
-    for (int k = 0; k < KB; ++k) {
-      const float wk = k < nb ? fast_exp2(lse[k] - Mu) : 0.f;
-      S += wk;
-      wl[64 * k + lane] = wk;
-    }
-    wl[64 * KB + lane] = resc;
-    M = Mn;
     // the weights were written by this wave's own lanes: its LDS operations complete in order
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int i = 64 * c + lane;
       if (i < nch) {
         const int row = i >> 4;
-        const float rs_ = wl[64 * KB + row];
+        const float rs_ = stat[row];
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[c][e] *= rs_;
+#pragma unroll 1
+        for (int k = 0; k < nb; ++k) {
+          const float w = lsea[k * R + row];
+          float f[8];
+          unpack_f16x8(*reinterpret_cast<const u32x4*>(oarea + k * part_bytes + 16 * i), f);
 #pragma unroll
-        for (int k = 0; k < KB; ++k) {
-          if (k < nb) {
-            const float wk = wl[64 * k + row];
-            float f[8];
-            unpack_f16x8(x[k][c], f);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[c][e] += wk * f[e];
-          }
+          for (int e = 0; e < 8; ++e) acc[c][e] += w * f[e];
         }
       }
     }
   }
-  wl[64 * (KB + 1) + lane] = S > 0.f ? 1.f / S : 0.f;
+  if (lane < R) stat[64 + lane] = S > 0.f ? 1.f / S : 0.f;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int i = 64 * c + lane;
     if (i < nch) {
       const int row = i >> 4;
-      const float inv = wl[64 * (KB + 1) + row];
+      const float inv = stat[64 + row];
       const int j = row / p.g;
       const int hq = row - j * p.g;
       u32x4 ov;
@@ -1284,17 +1273,17 @@ __device__ __forceinline__ void merge_parts(const AttnParams& p, __amdgpu_buffer
   }
 }
 
-// merge_parts for the row count of the launch: all loads of up to 32 parts (R <= 8) in flight.
+// merge_parts for the row count of the launch (chunks per lane: R * 16 / 64).
 template <int NT>
-__device__ __forceinline__ void merge_parts_for(const AttnParams& p, __amdgpu_buffer_rsrc_t rs, int b, int h,
-                                                const SeqParts& sp, float* wl) {
+__device__ __forceinline__ void merge_parts_for(const AttnParams& p, int b, int h, const SeqParts& sp, char* area,
+                                                int area_bytes) {
   if constexpr (NT == 1) {
     if (p.R <= 8)
-      merge_parts<2, 32>(p, rs, b, h, sp, wl);
+      merge_parts<2>(p, b, h, sp, area, area_bytes);
     else
-      merge_parts<4, 8>(p, rs, b, h, sp, wl);
+      merge_parts<4>(p, b, h, sp, area, area_bytes);
   } else {
-    merge_parts<4 * NT, 8 / NT>(p, rs, b, h, sp, wl);
+    merge_parts<4 * NT>(p, b, h, sp, area, area_bytes);
   }
 }
 
@@ -1484,8 +1473,8 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   // sequence it wrote a part of; the wave that brings a (sequence, head) counter to its part
   // count merges every part and re-arms the counter for the next call.  Nobody waits.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the partial stores are device-visible
-  const __amdgpu_buffer_rsrc_t rs = ws_rsrc(p);
-  float* wl = reinterpret_cast<float*>(lds) + h * 2304;  // tile buffers are free after the loop
+  // the tile buffers are free after the loop: a quarter of them per wave for its merges
+  char* area = lds + h * (2 * BUF / rows::NKV);
   // both arrivals in flight together, then the merges this wave completes
   int prev0 = 0, prev1 = 0;
   if (lane == 0) {
@@ -1505,7 +1494,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     const SeqParts sp = seq_parts(st, b, per);
     if ((k == 0 ? prev0 : prev1) != sp.np - 1) continue;
     if (lane == 0) __hip_atomic_store(p.ws_cnt + b * rows::NKV + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_parts_for<NT>(p, rs, b, h, sp, wl);
+    merge_parts_for<NT>(p, b, h, sp, area, 2 * BUF / rows::NKV);
   }
 }
 
