@@ -52,14 +52,29 @@ struct AttnParams {
   float scale_log2;  // softmax_scale * log2(e)
 };
 
+// Maxima of attention scores without IEEE-mode canonicalisation.  fmaxf on an MFMA result makes
+// the compiler quieten each operand first (v_max_f32 x, x, x); scores here are finite or -inf,
+// never NaN, so the raw v_max3_f32 / v_max_f32 give the same value in a third of the
+// instructions.
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float max_raw(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 // Reductions over the four lanes {l, l^16, l^32, l^48} that hold the same query row, with the
 // gfx950 row-swap permutes: permlane16_swap(x, x) hands lane l the pair {x[l], x[l^16]} and
 // permlane32_swap(x, x) the pair {x[l], x[l^32]} (no LDS round trip, unlike ds_bpermute).
 __device__ __forceinline__ float max_over_quads(float v) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  v = max_raw(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return max_raw(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 __device__ __forceinline__ float sum_over_quads(float v) {
@@ -344,28 +359,22 @@ __device__ __forceinline__ void compute_tile(const AttnParams& p, const KVTile<H
     // s[a][r]: score of token T0 + 8lq + 4a + r against query row li + 16nt.  Only tiles that
     // reach past some real row's last visible key pay for the mask (a wave-uniform test).
     float x[8];
-    float mx = -INFINITY;
     if (T0 + 31 > lim_min) {
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = T0 + 8 * lq + 4 * a + r;
-          const float v = (t <= lim[nt]) ? s[a][r] * p.scale_log2 : -INFINITY;
-          x[4 * a + r] = v;
-          mx = fmaxf(mx, v);
+          x[4 * a + r] = (t <= lim[nt]) ? s[a][r] * p.scale_log2 : -INFINITY;
         }
       }
     } else {
 #pragma unroll
-      for (int a = 0; a < 2; ++a) {
+      for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          x[4 * a + r] = s[a][r] * p.scale_log2;
-          mx = fmaxf(mx, x[4 * a + r]);
-        }
-      }
+        for (int r = 0; r < 4; ++r) x[4 * a + r] = s[a][r] * p.scale_log2;
     }
+    float mx = max3_raw(max3_raw(x[0], x[1], x[2]), max3_raw(x[3], x[4], x[5]), max_raw(x[6], x[7]));
     mx = max_over_quads(mx);
     const bool grow = mx > m_run[nt] + kRescaleSlack;
     if (__any(grow)) {
@@ -1739,8 +1748,8 @@ __device__ __forceinline__ void compute_tile_prefill(const AttnParams& p, const 
   bool grow_any = false;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    float m = fmaxf(fmaxf(fmaxf(s[nt][0][0], s[nt][0][1]), fmaxf(s[nt][0][2], s[nt][0][3])),
-                    fmaxf(fmaxf(s[nt][1][0], s[nt][1][1]), fmaxf(s[nt][1][2], s[nt][1][3])));
+    const float m = max3_raw(max3_raw(s[nt][0][0], s[nt][0][1], s[nt][0][2]),
+                             max3_raw(s[nt][0][3], s[nt][1][0], s[nt][1][1]), max_raw(s[nt][1][2], s[nt][1][3]));
     mx[nt] = max_over_quads(m) * p.scale_log2;
     grow_any |= mx[nt] > m_run[nt] + kRescaleSlack;
   }
