@@ -45,6 +45,7 @@ extern "C" {
 #define PKV_ENOSPC (-3)  /* workspace smaller than pkv_decode_workspace_bytes() */
 
 #define PKV_STATUS_BAD_PAGE 1
+#define PKV_STATUS_BAD_POSITION 2  /* a rotary position outside the cos/sin table (clamped) */
 
 /* pkv_decode_attn flags (0 = the library's choice of kernel and merge) */
 #define PKV_DECODE_TWO_PASS 1    /* merge split-K partials in a second launch */
@@ -166,6 +167,53 @@ int pkv_gather_pages(const uint64_t* src_bases, const uint64_t* dst_bases, int32
                      int64_t src_page_stride_bytes, int64_t dst_page_stride_bytes,
                      int64_t page_bytes, int32_t src_num_pages, int32_t dst_num_pages,
                      int32_t* status, void* stream);
+
+/*
+ * Pre-attention epilogue: QKV split, optional per-head RMSNorm (QK-norm) and rotary embedding,
+ * replacing engine/executor.py:108-118 / :143-150 (q = qkv[..., :qs].view(.., nh, hd),
+ * k, v likewise; fused_rms_norm(q, q_norm_w) and (k, k_norm_w) when the model has QK-norm;
+ * q * cos + rotate_half(q) * sin and the same for k, with cos/sin rows from the
+ * engine/executor.py:45-57 table).  For b < batch, j < s_new, token row
+ * qkv + b * qkv_sb + j * qkv_ss = [q (n_heads * head_dim) | k (n_kv * head_dim) | v (n_kv * head_dim)]
+ * at position positions[b] + j (row of cos_tab / sin_tab, bf16 [n_pos, head_dim]):
+ *   q_out[b, j, h] = rope(norm(q_h)), k_out[b, j, h] = rope(norm(k_h)) (k_out may be NULL),
+ * with the reference's bf16 rounding after each torch op, so the result is bit-exact against it
+ * (to a bf16 unit where QK-norm is on).  q_norm_w / k_norm_w NULL = no QK-norm.
+ * If k_cache/v_cache are non-NULL the rotated k and the unrotated v are also appended at
+ * slot cache_seqlens[b] + j, as pkv_append (the flash_attn_with_kvcache(k=, v=) append half),
+ * so the attention call that follows can pass k = v = NULL with cache_seqlens + s_new.
+ * Positions outside [0, n_pos) are clamped and flag PKV_STATUS_BAD_POSITION.
+ */
+int pkv_rope_qk(const void* qkv, int64_t qkv_sb, int64_t qkv_ss, const int32_t* positions,
+                const void* cos_tab, const void* sin_tab, int32_t n_pos,
+                const void* q_norm_w, const void* k_norm_w, float eps,
+                void* q_out, int64_t qo_sb, int64_t qo_ss, int64_t qo_sh,
+                void* k_out, int64_t ko_sb, int64_t ko_ss, int64_t ko_sh,
+                void* k_cache, void* v_cache, int64_t cache_page_stride,
+                const int32_t* block_table, int64_t bt_stride, const int32_t* cache_seqlens,
+                int32_t batch, int32_t s_new, int32_t n_heads, int32_t n_kv, int32_t head_dim,
+                int32_t page_size, int32_t num_pages, int32_t max_blocks,
+                int32_t* status, void* stream);
+
+/*
+ * RMSNorm over rows (engine/fused_kernels.py:31-65 fused_rms_norm; called at
+ * engine/executor.py:106, :122, :131): out[r] = bf16(h * rsqrt(mean(h^2) + eps) * weight) in
+ * fp32, h = x[r], or, when residual is non-NULL, h = bf16(x[r] + residual[r]) (the preceding
+ * `hidden = residual + ...` of engine/executor.py:121, :127), also stored to h_out if non-NULL.
+ * hidden a multiple of 8, at most 8192; rows 16-byte aligned.
+ */
+int pkv_rms_norm(const void* x, int64_t x_stride, const void* residual, int64_t r_stride,
+                 void* h_out, int64_t h_stride, const void* weight, void* out, int64_t o_stride,
+                 int64_t rows, int32_t hidden, float eps, void* stream);
+
+/*
+ * SiLU-gated MLP activation (engine/executor.py:127: F.silu(gu[..., :m]) * gu[..., m:], i.e.
+ * gate = gu, up = gu + m; the Triton engine/fused_kernels.py:8-28 fused_silu_mul(gate, up)):
+ * out[r, i] = bf16(bf16(silu(gate[r, i])) * up[r, i]) for i < m.  m a multiple of 8; rows
+ * 16-byte aligned (row strides in elements).
+ */
+int pkv_silu_mul(const void* gate, int64_t g_stride, const void* up, int64_t u_stride,
+                 void* out, int64_t o_stride, int64_t rows, int32_t m, void* stream);
 
 #ifdef __cplusplus
 }

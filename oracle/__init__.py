@@ -11,6 +11,8 @@ Modules
   page_ops         page copy / copy-on-write / gather-compaction restatements (bit-exact).
   kv_state         the FlashAttnKVCache allocator and PrefixCache state machines, restated
                    from engine/kv_cache.py and engine/prefix_cache.py without tensors.
+  epilogue         the elementwise steps around attention: rotary tables, QKV split + QK-norm +
+                   RoPE, RMSNorm with the residual add, SiLU(gate) * up.
 
 How each function is pinned (the checks live in tests/test_oracle.py):
   slot_mapping / append_kv     docs/architecture.md:140-147 worked example, hand-computed slots,
@@ -24,4 +26,10 @@ How each function is pinned (the checks live in tests/test_oracle.py):
   page_ops                     closed-form index arithmetic against per-element loops.
   kv_state                     golden traces recorded from the reference's own
                                engine/kv_cache.py / engine/prefix_cache.py (tests/golden/).
+  epilogue.rope_bf16           an element-by-element restatement with explicit bf16 rounding
+                               (bit-exact), the identity at position 0, the fp64 complex rotation
+                               (rope_f64) and norm preservation; rope_tables against math.cos/sin.
+  epilogue.rms_norm_f64        torch.nn.functional.rms_norm (fp64), constant rows (closed form),
+                               scale invariance.
+  epilogue.silu_mul_ref        torch.nn.functional.silu (fp64), silu(0) = 0 and the large-|g| limits.
 """

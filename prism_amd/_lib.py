@@ -19,6 +19,7 @@ PKV_EINVAL = -1
 PKV_EHIP = -2
 PKV_ENOSPC = -3
 PKV_STATUS_BAD_PAGE = 1
+PKV_STATUS_BAD_POSITION = 2
 PKV_DECODE_TWO_PASS = 1
 PKV_DECODE_FUSED_MERGE = 2
 PKV_DECODE_HEADS = 4
@@ -81,6 +82,24 @@ _SIGNATURES = {
         _I32, _I32,
         _P, _P,
     ]),
+    "pkv_rope_qk": (c_int32, [
+        _P, _I64, _I64, _P,              # qkv + strides, positions
+        _P, _P, _I32,                    # cos, sin, n_pos
+        _P, _P, c_float,                 # q_norm_w, k_norm_w, eps
+        _P, _I64, _I64, _I64,            # q_out
+        _P, _I64, _I64, _I64,            # k_out
+        _P, _P, _I64,                    # caches
+        _P, _I64, _P,                    # block table, seqlens
+        _I32, _I32, _I32, _I32, _I32,    # batch, s_new, n_heads, n_kv, head_dim
+        _I32, _I32, _I32,                # page_size, num_pages, max_blocks
+        _P, _P,                          # status, stream
+    ]),
+    "pkv_rms_norm": (c_int32, [
+        _P, _I64, _P, _I64, _P, _I64,    # x, residual, h_out
+        _P, _P, _I64,                    # weight, out
+        _I64, _I32, c_float, _P,         # rows, hidden, eps, stream
+    ]),
+    "pkv_silu_mul": (c_int32, [_P, _I64, _P, _I64, _P, _I64, _I64, _I32, _P]),
 }
 
 _lock = threading.Lock()

@@ -379,7 +379,10 @@ __device__ __forceinline__ void compute_tile(const AttnParams& p, const KVTile<H
     const bool grow = mx > m_run[nt] + kRescaleSlack;
     if (__any(grow)) {
       const float m_new = grow ? mx : m_run[nt];
-      const float alpha = fast_exp2(m_run[nt] - m_new);  // 0 on the first visible tile, 1 if unchanged
+      // 0 on a row's first visible tile, 1 if unchanged; a row that has seen no key yet keeps
+      // -inf while other rows grow (split-K parts of speculative verify that start past its last
+      // visible key), and -inf - -inf would make its state NaN
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[nt] - m_new);
       l_run[nt] *= alpha;
 #pragma unroll
       for (int n = 0; n < DPL; ++n) acc[nt][n] *= alpha;
@@ -689,8 +692,9 @@ __global__ __launch_bounds__(64 * W, PKV_DECODE_MIN_BLOCKS) void decode_kernel(c
 
 // Two-pass mode: the split-K merge as its own launch.  The kernel boundary orders the partial
 // stores before these loads, so plain vector loads serve, and every split's loads of a thread are
-// issued before any is used: one memory round trip per kMergeBatch splits.  Grid (n_kv, batch);
-// thread t of the workgroup owns (row, 4 head-dim elements) = (t / (HD/4), t % (HD/4)).
+// issued before any is used: one memory round trip per kMergeBatch splits.  Grid (n_kv, batch,
+// groups of 16 query rows); thread t of the workgroup owns (row, 4 head-dim elements) =
+// (16 blockIdx.z + t / (HD/4), t % (HD/4)).
 constexpr int kMergeBatch = 32;
 
 template <int HD>
@@ -704,8 +708,10 @@ __global__ __launch_bounds__(512) void combine_kernel(const AttnParams p) {
   seq_lengths(p, b, c, L);
   const int n_split = num_splits(p, L);
   if (n_split <= 1) return;
-  const int row = threadIdx.x / Q4;
-  const int d0 = (threadIdx.x - row * Q4) * 4;
+  const int rg = int(blockIdx.z) * 16;  // this workgroup's 16 query rows: rg .. rg + 15
+  const int lr = threadIdx.x / Q4;
+  const int row = rg + lr;
+  const int d0 = (threadIdx.x - lr * Q4) * 4;
   const bool active = row < p.R;
   const int64_t base = int64_t(b * p.n_kv + h) * p.max_splits * p.R;
   if (threadIdx.x < 16) {
@@ -723,8 +729,8 @@ __global__ __launch_bounds__(512) void combine_kernel(const AttnParams p) {
     // (m, l) of every (split, row) of the batch into LDS, one pair per thread
     {
       const int u = threadIdx.x / 16, r = threadIdx.x % 16;
-      const bool ok = u < ns && r < p.R;
-      const f32x2 ml = ok ? *reinterpret_cast<const f32x2*>(p.ws_ml + (base + int64_t(s0 + u) * p.R + r) * 2)
+      const bool ok = u < ns && rg + r < p.R;
+      const f32x2 ml = ok ? *reinterpret_cast<const f32x2*>(p.ws_ml + (base + int64_t(s0 + u) * p.R + rg + r) * 2)
                           : f32x2{-INFINITY, 0.f};
       sm_m_in[u][r] = ml[0];
       sm_l_in[u][r] = ml[1];
@@ -748,15 +754,15 @@ __global__ __launch_bounds__(512) void combine_kernel(const AttnParams p) {
     }
     __syncthreads();
     if (active) {
-      o *= sm_rescale[row];
+      o *= sm_rescale[lr];
 #pragma unroll
       for (int u = 0; u < kMergeBatch; ++u)
-        if (u < ns) o += sm_m_in[u][row] * x[u];
+        if (u < ns) o += sm_m_in[u][lr] * x[u];
     }
     __syncthreads();  // the batch's weights are consumed before the next batch overwrites them
   }
   if (active) {
-    const float inv = sm_l[row] > 0.f ? 1.f / sm_l[row] : 0.f;
+    const float inv = sm_l[lr] > 0.f ? 1.f / sm_l[lr] : 0.f;
     const int j = row / p.g;
     const int hq = row - j * p.g;
     const u32x2 ov = {pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv)};
@@ -1757,7 +1763,7 @@ __device__ __forceinline__ void compute_tile_prefill(const AttnParams& p, const 
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const float m_new = mx[nt] > m_run[nt] + kRescaleSlack ? mx[nt] : m_run[nt];
-      const float alpha = fast_exp2(m_run[nt] - m_new);
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[nt] - m_new);  // see compute_tile
       l_run[nt] *= alpha;
 #pragma unroll
       for (int n = 0; n < DPL; ++n) acc[nt][n] *= alpha;
@@ -2064,7 +2070,8 @@ static void launch_decode_t(const AttnParams& p, int batch, hipStream_t stream) 
   // upper bound of the dense item count; items past the real total exit at once
   const int64_t items = int64_t(batch) * p.n_kv * p.max_splits;
   decode_kernel<HD, NT, W><<<dim3(unsigned(items)), 64 * W, 0, stream>>>(p);
-  if (p.two_pass && p.max_splits > 1) combine_kernel<HD><<<dim3(p.n_kv, batch), 512, 0, stream>>>(p);
+  if (p.two_pass && p.max_splits > 1)
+    combine_kernel<HD><<<dim3(p.n_kv, batch, (p.R + 15) / 16), 512, 0, stream>>>(p);
 }
 
 template <int HD>

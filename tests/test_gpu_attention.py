@@ -25,12 +25,15 @@ def _run_and_check(gpu, *, batch, ctx, page_size, n_kv, n_heads, head_dim, s_q, 
     kw = dict(cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"], causal=causal)
     k = dev["k"] if append else None
     v = dev["v"] if append else None
+    # NaN-filled output: a row the kernels fail to write cannot pass on stale values of an
+    # earlier call that the caching allocator hands back
+    out = torch.full_like(dev["q"], float("nan"))
     if kernel == "prefill":
-        out = prism_amd.prefill_attention(dev["q"], dev["k_cache"], dev["v_cache"], k, v, **kw)
+        out = prism_amd.prefill_attention(dev["q"], dev["k_cache"], dev["v_cache"], k, v, out=out, **kw)
     else:
         out = prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], k, v,
                                                 split_tokens=split_tokens, two_pass=two_pass,
-                                                kernel=kernel, grid=grid, **kw)
+                                                kernel=kernel, grid=grid, out=out, **kw)
     torch.cuda.synchronize()
     ref, kb, vb = pa.flash_attn_with_kvcache_ref(
         cpu["q"], cpu["k_cache"], cpu["v_cache"], cpu["k"] if append else None, cpu["v"] if append else None,
@@ -133,6 +136,18 @@ def test_per_head_kernel_on_balanced_shapes(gpu, case):
     for two_pass in (False, True):
         _run_and_check(gpu, batch=B, ctx=ctx, page_size=P, n_kv=n_kv, n_heads=nh, head_dim=hd, s_q=s_q,
                        kernel="heads", two_pass=two_pass, what=f"heads{case}")
+
+
+@pytest.mark.parametrize("kernel", ["auto", "heads"])
+@pytest.mark.parametrize("two_pass", [True, False])
+def test_verify_part_holding_only_keys_a_row_cannot_see(gpu, kernel, two_pass):
+    # speculative verify (s_q > 1) with a split-K part that starts past some query rows' last
+    # visible key: those rows keep a -inf running max while the other rows of their wave rescale
+    # (a part per 32-token tile on the balanced kernel's default grid, 512-token splits per head)
+    for i, (ctx, s_q, append) in enumerate([([259], 4, False), ([513, 1027], 4, False), ([1025], 2, False),
+                                            ([1023, 252], 4, True), ([509, 1019, 3], 5, True)]):
+        _run_and_check(gpu, batch=len(ctx), ctx=ctx, page_size=256, n_kv=4, n_heads=28, head_dim=128, s_q=s_q,
+                       append=append, kernel=kernel, two_pass=two_pass, seed=i, what=f"verify-edge{i}")
 
 
 def test_batch_beyond_balanced_limit(gpu):

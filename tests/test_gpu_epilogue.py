@@ -1,0 +1,134 @@
+"""GPU parity of the pre-attention epilogue (QKV split + QK-norm + RoPE + paged append), RMSNorm and
+SiLU-mul against oracle/epilogue.py, through the C ABI.  RoPE and the appended cache rows are
+bit-exact (the reference's bf16 expression is exact in fp32 up to its roundings); QK-norm, RMSNorm
+and SiLU-mul agree to one bf16 unit (rsqrt / exp differ in the last fp32 bits)."""
+import numpy as np
+import pytest
+import torch
+
+import prism_amd
+from oracle import epilogue as ep
+from oracle import paged_attention as pa
+from pkv_testutil import assert_attn_close, make_paged_case
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand(shape, seed, scale=1.0, device="cpu"):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(torch.bfloat16).to(device)
+
+
+def _ulp_close(got: torch.Tensor, ref: np.ndarray, what: str, ulps: float = 1.0):
+    """|got - ref| <= ulps bf16 units of ref (2^-8 relative, with a floor for tiny values)."""
+    g = got.float().cpu().numpy().astype(np.float64)
+    tol = ulps * np.maximum(np.abs(ref), 1e-30) * 2.0 ** -7 + 1e-30
+    bad = np.abs(g - ref) > tol
+    assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} beyond {ulps} bf16 unit(s), max diff {np.max(np.abs(g - ref)):.3g}"
+
+
+ROPE_CASES = [
+    # (batch, s_new, n_heads, n_kv, head_dim, qk_norm)
+    (32, 1, 28, 4, 128, False),   # 7B decode
+    (3, 37, 40, 8, 128, False),   # 14B chunk
+    (4, 5, 14, 2, 64, False),     # 0.5B verify
+    (2, 9, 16, 8, 128, True),     # QK-norm (Qwen3-style)
+    (1, 3, 14, 2, 64, True),
+]
+
+
+@pytest.mark.parametrize("case", ROPE_CASES, ids=[f"r{i}" for i in range(len(ROPE_CASES))])
+def test_rope_qk_matches_reference_expression(gpu, case):
+    B, s, nh, nkv, hd, qkn = case
+    print(f"rope case {case}", flush=True)
+    qkv = _rand((B, s, (nh + 2 * nkv) * hd), 11 + B, 2.0)
+    pos = np.array([(97 * b + 5) % 5000 for b in range(B)], dtype=np.int32)
+    cos, sin = ep.rope_tables(hd, 5100)
+    qw = _rand((hd,), 1) if qkn else None
+    kw = _rand((hd,), 2) if qkn else None
+    q_ref, k_ref, _ = ep.qkv_split_rope(qkv, pos, cos, sin, nh, nkv, qw, kw)
+    dcos, dsin = cos.to(gpu), sin.to(gpu)
+    q, k = prism_amd.rope_qk(qkv.to(gpu), torch.from_numpy(pos).to(gpu), dcos, dsin, nh, nkv,
+                             q_norm_w=qw.to(gpu) if qkn else None, k_norm_w=kw.to(gpu) if qkn else None)
+    torch.cuda.synchronize()
+    if not qkn:
+        assert torch.equal(q.cpu(), q_ref), "q not bit-exact"
+        assert torch.equal(k.cpu(), k_ref), "k not bit-exact"
+    else:
+        # one-unit differences of the normalised inputs can move the rotated value by a little more
+        _ulp_close(q, q_ref.double().numpy(), "q (QK-norm)", 3.0)
+        _ulp_close(k, k_ref.double().numpy(), "k (QK-norm)", 3.0)
+
+
+def test_rope_qk_appends_into_pages_then_attends(gpu):
+    # the fused epilogue's append + attention without k/v equals attention with the reference path
+    B, s, nh, nkv, hd, P = 3, 4, 28, 4, 128, 256
+    ctx = [0, 300, 1023]
+    cpu, dev = make_paged_case(gpu, batch=B, ctx=ctx, page_size=P, n_kv=nkv, n_heads=nh, head_dim=hd, s_q=s,
+                               seed=5)
+    qkv = _rand((B, s, (nh + 2 * nkv) * hd), 21, 1.0)
+    pos = np.array(ctx, dtype=np.int32)
+    cos, sin = ep.rope_tables(hd, 2048)
+    q_ref, k_ref, v_ref = ep.qkv_split_rope(qkv, pos, cos, sin, nh, nkv)
+    ref, kb, vb = pa.flash_attn_with_kvcache_ref(q_ref, cpu["k_cache"], cpu["v_cache"], k_ref, v_ref,
+                                                 cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"],
+                                                 causal=True)
+    dcos, dsin = cos.to(gpu), sin.to(gpu)
+    sl = dev["cache_seqlens"]
+    q, _ = prism_amd.rope_qk(qkv.to(gpu), sl, dcos, dsin, nh, nkv, return_k=False, k_cache=dev["k_cache"],
+                             v_cache=dev["v_cache"], block_table=dev["block_table"], cache_seqlens=sl)
+    out = prism_amd.flash_attn_with_kvcache(q, dev["k_cache"], dev["v_cache"], cache_seqlens=sl + s,
+                                            block_table=dev["block_table"], causal=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(pa.bf16_bits(dev["k_cache"]), kb), "appended K not bit-exact"
+    assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "appended V not bit-exact"
+    assert_attn_close(out, ref, "rope+append+attention")
+    assert prism_amd.read_status(gpu) == 0
+
+
+def test_device_rope_tables_match_the_cpu_formula(gpu):
+    # the reference builds its tables on the device (engine/executor.py:49-55); device and host
+    # cos / sin may differ in the last fp32 bit, so bf16 entries agree to one unit
+    for hd in (64, 128):
+        cos, sin = ep.rope_tables(hd, 6000)
+        dcos, dsin = prism_amd.rope_tables(hd, 6000, device=gpu)
+        for name, a, b in (("cos", dcos, cos), ("sin", dsin, sin)):
+            diff = (a.float().cpu() - b.float()).abs()
+            assert float(diff.max()) <= 2.0 ** -8 * 1.01, f"{name} hd={hd}: max diff {float(diff.max())}"
+            assert float((diff == 0).float().mean()) > 0.99, f"{name} hd={hd}: too many differing entries"
+
+
+def test_rope_qk_flags_positions_past_the_table(gpu):
+    qkv = _rand((2, 2, 8 * 64), 3).to(gpu)
+    cos, sin = prism_amd.rope_tables(64, 16, device=gpu)
+    prism_amd.rope_qk(qkv, torch.tensor([3, 15], dtype=torch.int32, device=gpu), cos, sin, 4, 2)
+    assert prism_amd.read_status(gpu) == 2
+    with pytest.raises(RuntimeError):
+        prism_amd.rope_qk(qkv[..., :-8], 0, cos, sin, 4, 2)
+
+
+@pytest.mark.parametrize("hidden,rows,resid", [(3584, 33, False), (5120, 7, True), (896, 1, True), (8192, 3, False)])
+def test_rms_norm_matches_fp64(gpu, hidden, rows, resid):
+    x = _rand((rows, hidden), hidden + rows, 3.0)
+    w = _rand((hidden,), 4)
+    r = _rand((rows, hidden), 5) if resid else None
+    ref, h_ref = ep.rms_norm_f64(x.float().numpy(), w.float().numpy(), 1e-6,
+                                 r.float().numpy() if resid else None)
+    res = prism_amd.rms_norm(x.to(gpu), w.to(gpu), 1e-6, residual=r.to(gpu) if resid else None)
+    torch.cuda.synchronize()
+    out = res[0] if resid else res
+    _ulp_close(out, ep.round_bf16(ref), f"rms_norm {hidden}x{rows}", 1.0)
+    if resid:
+        assert np.array_equal(res[1].float().cpu().numpy(), h_ref), "residual sum not bit-exact"
+
+
+def test_silu_mul_matches_reference(gpu):
+    rows, m = 37, 18944
+    gu = _rand((rows, 2 * m), 9, 3.0)
+    ref = ep.silu_mul_ref(gu[:, :m].float().numpy(), gu[:, m:].float().numpy())
+    d = gu.to(gpu)
+    out = prism_amd.silu_mul(d[:, :m], d[:, m:])
+    torch.cuda.synchronize()
+    _ulp_close(out, ref, "silu_mul", 1.0)
+    exact = np.mean(out.float().cpu().numpy() == ref)
+    assert exact > 0.99, f"only {exact:.4f} of outputs bit-exact"
