@@ -16,7 +16,9 @@ bytes per step / step time (GB/s), the per-call roofline (step time / layers) an
 
 --workload config2 / config4 / config5 measures the other configurations the same way (decode at
 b=8 ctx 2048; 14B chunked prefill, MFMA-bound, in TFLOP/s; 7B shared-prefix speculative verify,
-plus its copy-on-write and a compaction of every live page into a fresh pool).
+plus its copy-on-write and a compaction of every live page into a fresh pool).  --workload
+epilogue times the elementwise kernels on either side of attention (QKV split + RoPE + paged
+append, RMSNorm with the residual add, SiLU-mul) at the 14B prefill-chunk and 7B decode scales.
 """
 from __future__ import annotations
 
@@ -42,7 +44,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--workload", choices=["config2", "config3", "config4", "config5"], default="config3")
+    ap.add_argument("--workload", choices=["config2", "config3", "config4", "config5", "epilogue"], default="config3")
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = library choice)")
     ap.add_argument("--layers", type=int, default=0, help="layers (0 = the model's)")
     ap.add_argument("--merge", choices=["auto", "two-pass", "fused"], default="auto",
@@ -193,6 +195,118 @@ def config5_page_ops(prism_amd, w, dev) -> dict:
     return out
 
 
+def epilogue_bench(args, dev) -> dict:
+    """QKV split + RoPE + paged append, residual add + RMSNorm and SiLU-mul per layer: 20 calls over
+    8 per-layer buffer sets (8 x 100-340 MB at the prefill scale: the 256 MB Infinity Cache cannot
+    serve a repeat) captured in a HIP graph and replayed, HIP events around the replays.  Bytes are the algorithmic ones: every input
+    element read once, every output written once (cos / sin: one table row per token)."""
+    import torch
+
+    import prism_amd
+
+    sets = 8
+    scales = {
+        # name: (model, tokens as (B, s), n_heads, n_kv, hidden, intermediate, page_size, pool pages)
+        "prefill14b": ("Qwen2.5-14B chunk 8x512", (8, 512), 40, 8, 5120, 13824),
+        "decode7b": ("Qwen2.5-7B decode b=32", (32, 1), 28, 4, 3584, 18944),
+    }
+    hd, P = 128, 256
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    res = {}
+    for key, (model, (B, s), nh, nkv, H, M) in scales.items():
+        T = B * s
+        width = (nh + 2 * nkv) * hd
+        pages_per_seq = -(-(4096 + s) // P)
+        n_pages = B * pages_per_seq
+        cos, sin = prism_amd.rope_tables(hd, 4096 + s, device=dev)
+        pos = torch.randint(0, 4096, (B,), generator=g, device=dev, dtype=torch.int32)
+        bufs = []
+        for _ in range(sets):
+            kc = torch.zeros(n_pages, P, nkv, hd, dtype=torch.bfloat16, device=dev)
+            bufs.append(dict(
+                qkv=torch.randn(B, s, width, generator=g, device=dev).to(torch.bfloat16),
+                q=torch.empty(B, s, nh, hd, dtype=torch.bfloat16, device=dev),
+                kc=kc, vc=torch.zeros_like(kc),
+                x=torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16),
+                r=torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16),
+                o=torch.empty(T, H, dtype=torch.bfloat16, device=dev),
+                h=torch.empty(T, H, dtype=torch.bfloat16, device=dev),
+                gu=torch.randn(T, 2 * M, generator=g, device=dev).to(torch.bfloat16),
+                a=torch.empty(T, M, dtype=torch.bfloat16, device=dev)))
+        w = torch.randn(H, generator=g, device=dev).to(torch.bfloat16)
+        bt = torch.randperm(n_pages, generator=g, device=dev).to(torch.int32).view(B, pages_per_seq)
+        sl = pos.clone()
+        ops = {
+            "rope_qk_append": (lambda b: prism_amd.rope_qk(b["qkv"], pos, cos, sin, nh, nkv, return_k=False,
+                                                           q_out=b["q"], k_cache=b["kc"], v_cache=b["vc"],
+                                                           block_table=bt, cache_seqlens=sl),
+                               T * (width + 2 * hd + nh * hd + 2 * nkv * hd) * 2),
+            "add_rms_norm": (lambda b: prism_amd.rms_norm(b["x"], w, 1e-6, residual=b["r"], out=b["o"], h_out=b["h"]),
+                             (4 * T * H + H) * 2),
+            "silu_mul": (lambda b: prism_amd.silu_mul(b["gu"][:, :M], b["gu"][:, M:], out=b["a"]), 3 * T * M * 2),
+        }
+        out = {"model": model, "tokens": T}
+        for name, (fn, nbytes) in ops.items():
+            reps = 20
+
+            def calls(fn=fn):
+                for i in range(reps):
+                    fn(bufs[i % sets])
+
+            # replayed as one HIP graph of 20 calls: the time is the kernels', not Python's
+            us = time_graph(calls, argparse.Namespace(warmup=2, steps=5), dev) * 1e3 / reps
+            out[name] = {"us": round(us, 2), "bytes": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                         "pct_of_peak_hbm": round(100 * nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2)}
+            print(f"[bench] {key} {name}: {us:.2f} us, {out[name]['gbs']} GB/s", file=sys.stderr, flush=True)
+        res[key] = out
+        del bufs
+        torch.cuda.empty_cache()
+    if prism_amd.read_status(dev):
+        print("[bench] WARNING: kernel status flags set", file=sys.stderr)
+    return res
+
+
+def epilogue_cpu_baseline(seed: int) -> dict:
+    """The reference's eager torch expressions on the host cores (engine/executor.py:108-127 with
+    the Triton norms restated in torch), on 1/8 of the 14B chunk (512 tokens)."""
+    import torch
+
+    from oracle import epilogue as ep
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(seed)
+    T, nh, nkv, hd, H, M = 512, 40, 8, 128, 5120, 13824
+    qkv = torch.randn(1, T, (nh + 2 * nkv) * hd, generator=g).to(torch.bfloat16)
+    cos, sin = ep.rope_tables(hd, 4096 + T)
+    pos = torch.tensor([1000], dtype=torch.int32)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    r = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w = torch.randn(H, generator=g).to(torch.bfloat16)
+    gu = torch.randn(T, 2 * M, generator=g).to(torch.bfloat16)
+
+    def run():
+        ep.cpu_epilogue_ref(qkv, pos, cos, sin, nh, nkv)
+        hsum = r + x
+        hf = hsum.float()
+        (hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + 1e-6) * w.float()).to(torch.bfloat16)
+        torch.nn.functional.silu(gu[:, :M]) * gu[:, M:]
+
+    for _ in range(2):
+        run()
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    width = (nh + 2 * nkv) * hd
+    nbytes = T * (width + 2 * hd + nh * hd + 2 * nkv * hd) * 2 + (4 * T * H + H) * 2 + 3 * T * M * 2
+    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"the three steps on 512 of the chunk's 4096 tokens (14B shape), eager torch CPU bf16; "
+                      f"2 warm-ups, median of 5; torch {torch.__version__}"}
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -207,6 +321,32 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.workload == "epilogue":
+        res = epilogue_bench(args, dev)
+        pf = res["prefill14b"]
+        names = ("rope_qk_append", "add_rms_norm", "silu_mul")
+        tot_b = sum(pf[n]["bytes"] for n in names)
+        tot_us = sum(pf[n]["us"] for n in names)
+        dom = max(names, key=lambda n: pf[n]["bytes"])
+        result = {
+            "metric": "attention epilogue kernels HBM GB/s (% of peak), Qwen2.5-14B prefill chunk 8x512 per layer",
+            "value": round(tot_b / (tot_us * 1e-6) / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": 20,
+            "warmup": 1, "ms_per_step": round(tot_us / 1e3, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "epilogue: QKV split + RoPE + paged append, residual add + RMSNorm, SiLU-mul "
+                                   "per layer at the 14B prefill chunk (4096 tokens) and the 7B decode batch "
+                                   "(32 tokens)", "seed": args.seed},
+            "roofline": {"bound": "hbm", "achieved": pf[dom]["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(pf[dom]["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": f"{dom} (the largest of the three) at the 14B prefill chunk; HIP events around "
+                                   "graph replays of 20 calls over 8 per-layer buffer sets",
+                         "bytes_per_call": pf[dom]["bytes"], "avg_call_us": pf[dom]["us"]},
+            "kernels": res,
+        }
+        if not args.no_cpu_baseline:
+            result["cpu_baseline"] = epilogue_cpu_baseline(args.seed)
+        print(json.dumps(result), flush=True)
+        return 0
     print(f"[bench] building {args.workload} workload (seed={args.seed})", file=sys.stderr, flush=True)
     w = getattr(workloads, args.workload)(dev, seed=args.seed, layers=args.layers or None)
     L = w.layers
