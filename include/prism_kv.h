@@ -104,6 +104,8 @@ size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, i
  * Otherwise a per-(sequence, KV head, split) kernel reduces split_tokens keys (a multiple of 32;
  * 0 = 512) per workgroup and merges the splits inside the launch (PKV_DECODE_TWO_PASS: in a
  * second launch).  Results agree up to rounding (fp32 order, fp16 split-K partials).
+ * The balanced kernel keeps each split's normalised output in fp16, so it needs |V| < 65504
+ * (bf16 V beyond that overflows the partial to inf); PKV_DECODE_HEADS keeps fp32 partials.
  * workspace must hold pkv_decode_workspace_bytes() bytes and be
  * zero-filled before its first use; every call leaves it in that state again (its first 64 KiB
  * hold per-(sequence, KV head) arrival counters, so batch * n_kv <= 16384 when a sequence can

@@ -14,7 +14,7 @@ Modules
   epilogue         the elementwise steps around attention: rotary tables, QKV split + QK-norm +
                    RoPE, RMSNorm with the residual add, SiLU(gate) * up.
 
-How each function is pinned (the checks live in tests/test_oracle.py):
+How each function is pinned (tests/test_oracle.py; the epilogue in tests/test_epilogue_oracle.py):
   slot_mapping / append_kv     docs/architecture.md:140-147 worked example, hand-computed slots,
                                a per-token brute-force loop, and the flash_attn docstring's layout.
   attention_fp64               torch SDPA (fp64, enable_gqa) on s_q == s_k where top-left and
