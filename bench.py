@@ -19,6 +19,8 @@ b=8 ctx 2048; 14B chunked prefill, MFMA-bound, in TFLOP/s; 7B shared-prefix spec
 plus its copy-on-write and a compaction of every live page into a fresh pool).  --workload
 epilogue times the elementwise kernels on either side of attention (QKV split + RoPE + paged
 append, RMSNorm with the residual add, SiLU-mul) at the 14B prefill-chunk and 7B decode scales.
+--workload tables times the per-step host staging of a graph-captured decode batch (block table,
+lengths, rotary rows) at config 3's batch: DecodeBatch against the reference's refill.
 """
 from __future__ import annotations
 
@@ -44,7 +46,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--workload", choices=["config2", "config3", "config4", "config5", "epilogue"], default="config3")
+    ap.add_argument("--workload", choices=["config2", "config3", "config4", "config5", "epilogue", "tables"], default="config3")
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = library choice)")
     ap.add_argument("--layers", type=int, default=0, help="layers (0 = the model's)")
     ap.add_argument("--merge", choices=["auto", "two-pass", "fused"], default="auto",
@@ -307,6 +309,129 @@ def epilogue_cpu_baseline(seed: int) -> dict:
                       f"2 warm-ups, median of 5; torch {torch.__version__}"}
 
 
+def tables_bench(args, dev) -> dict:
+    """Per-step staging of a captured decode batch's inputs at config 3's batch (Qwen2.5-7B shape,
+    32 sequences, context lognormal(1500, 1), 2043-page pool with a shuffled free list), each path
+    running decode steps of one token per sequence from the same start:
+
+      DecodeBatch      step() + advance(): grow, one packet of changed lengths / pages, one H2D
+                       copy, one pkv_table_update launch (rotary positions are cache_seqlens)
+      drop-in          the executor's refill (engine/executor.py:345-356: grow, build_block_table,
+                       zero + copy the static bt / sl, one cos / sin row copy per sequence) on
+                       prism_amd's build_block_table (one H2D copy of the whole table)
+      reference        the same refill on the reference's element-by-element build_block_table
+                       (engine/kv_cache.py:147-151, restated in the oracle), on device tensors
+
+    Host wall clock around the steps with a device synchronisation at the end (so copies and
+    launches are included), median of 3 runs."""
+    import numpy as np
+    import torch
+
+    import prism_amd
+    from oracle.kv_state import graph_staging_elementwise
+    from prism_amd import workloads
+
+    s = workloads.SHAPES["7B"]
+    mp = workloads.pages_for_budget(30.0, s["layers"], s["n_kv"], s["head_dim"])
+    ctx = workloads.lognormal_ctx(np.random.default_rng(args.seed), 32)
+    B, hd = len(ctx), s["head_dim"]
+    cos, sin = prism_amd.rope_tables(hd, 40000, device=dev)
+
+    def fresh_cache():
+        kv = prism_amd.FlashAttnKVCache(1, s["n_kv"], hd, mp, workloads.PAGE, str(dev))
+        kv.free_pages = [int(p) for p in np.random.default_rng(args.seed + 1).permutation(mp)]
+        for b, c in enumerate(ctx):
+            kv.new_sequence(b)
+            kv.seq_len[b] = 0
+            kv._ensure_capacity(b, int(c))
+            kv.seq_len[b] = int(c)
+        return kv
+
+    ids = list(range(B))
+
+    def run_decode_batch(n):
+        kv = fresh_cache()
+        db = prism_amd.DecodeBatch(kv, max_batch=B)
+        db.step(ids, 1, graph_batch=B)
+        db.advance()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            db.step(ids, 1, graph_batch=B)
+            db.advance()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e6
+
+    def run_refill(n, elementwise):
+        kv = fresh_cache()
+        g_bt = torch.zeros(B, 32, dtype=torch.int32, device=dev)   # engine/executor.py:282
+        g_sl = torch.zeros(B, dtype=torch.int32, device=dev)
+        g_cos = torch.zeros(B, 1, hd, dtype=torch.bfloat16, device=dev)
+        g_sin = torch.zeros(B, 1, hd, dtype=torch.bfloat16, device=dev)
+        bt_buf = torch.zeros(B, 32, dtype=torch.int32, device=dev)  # build_block_table's buffers
+        sl_buf = torch.zeros(B, dtype=torch.int32, device=dev)
+
+        def one():
+            for sid in ids:
+                kv._ensure_capacity(sid, kv.seq_len[sid] + 1)
+            if elementwise:
+                graph_staging_elementwise(bt_buf, sl_buf, g_bt, g_sl, kv.seq_pages, kv.seq_len, ids,
+                                          cos, sin, g_cos, g_sin)
+            else:
+                bt, sl = kv.build_block_table(ids)
+                nb = bt.shape[1]
+                g_bt[:] = 0
+                g_bt[:B, :nb] = bt
+                g_sl[:] = 0
+                g_sl[:B] = sl
+                for i, sid in enumerate(ids):
+                    g_cos[i, 0].copy_(cos[kv.seq_len[sid]])
+                    g_sin[i, 0].copy_(sin[kv.seq_len[sid]])
+            for sid in ids:
+                kv.seq_len[sid] += 1
+
+        one()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            one()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e6
+
+    ours = statistics.median(run_decode_batch(512) for _ in range(3))
+    print(f"[bench] DecodeBatch {ours:.1f} us/step", file=sys.stderr, flush=True)
+    drop_in = statistics.median(run_refill(128, False) for _ in range(3))
+    print(f"[bench] drop-in refill {drop_in:.1f} us/step", file=sys.stderr, flush=True)
+    ref = None
+    if not args.no_cpu_baseline:
+        ref = statistics.median(run_refill(16, True) for _ in range(3))
+        print(f"[bench] reference refill {ref:.1f} us/step", file=sys.stderr, flush=True)
+
+    # device time of one table update (32 lengths + 1 page entry): 20 launches on the uploaded
+    # packet captured in a HIP graph and replayed (host launch overhead excluded)
+    kv = fresh_cache()
+    db = prism_amd.DecodeBatch(kv, max_batch=B)
+    db.step(ids, 1, graph_batch=B)
+    packet = np.concatenate([np.stack([np.arange(B), np.asarray(ctx, dtype=np.int64)], 1).ravel(),
+                             np.array([0, 0, kv.seq_pages[0][0]])]).astype(np.int32)
+    db.apply(packet, B, 1)
+    lib = prism_amd._lib.load()
+    st = prism_amd.status_tensor(dev)
+
+    def launches():
+        for _ in range(20):
+            rc = lib.pkv_table_update(db._packet_dev.data_ptr(), B, 1, db.block_table.data_ptr(),
+                                      db.block_table.stride(0), db.cache_seqlens.data_ptr(), B, db.max_blocks,
+                                      mp, st.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+            prism_amd._lib.check(rc, "pkv_table_update")
+
+    upd_us = time_graph(launches, argparse.Namespace(warmup=2, steps=10), dev) * 1e3 / 20
+    return {"decode_batch_us": round(ours, 1), "drop_in_us": round(drop_in, 1),
+            "reference_us": None if ref is None else round(ref, 1), "update_us": round(upd_us, 2),
+            "packet_bytes": int(packet.nbytes), "batch": B, "pool_pages": mp,
+            "max_pages_per_seq": max(len(kv.seq_pages[b]) for b in ids)}
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -345,6 +470,35 @@ def main() -> int:
         }
         if not args.no_cpu_baseline:
             result["cpu_baseline"] = epilogue_cpu_baseline(args.seed)
+        print(json.dumps(result), flush=True)
+        return 0
+    if args.workload == "tables":
+        res = tables_bench(args, dev)
+        result = {
+            "metric": "decode-step input staging us per step (block table, lengths, rotary rows), "
+                      "Qwen2.5-7B b=32, 2043-page pool",
+            "value": res["decode_batch_us"], "unit": "us/step", "n_gpus": 1, "steps": 512, "warmup": 1,
+            "ms_per_step": round(res["decode_batch_us"] / 1e3, 4), "higher_is_better": False, "scaling": "weak",
+            "vs_baseline": None, "dtype": "int32", "data": "synthetic",
+            "config": {"workload": "tables: DecodeBatch.step + advance per decode step of 32 sequences (config 3 "
+                                   "lengths), against the executor's per-step refill of its graph buffers",
+                       "seed": args.seed},
+            # a few hundred bytes per launch: the update kernel is launch-bound, not HBM-bound
+            "roofline": {"bound": "hbm", "achieved": round(res["packet_bytes"] * 2 / (res["update_us"] * 1e-6) / 1e9, 4),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(res["packet_bytes"] * 2 / (res["update_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 8),
+                         "traffic": None,
+                         "kernel": "pkv_table_update (32 lengths + 1 page entry: packet read + entries written); "
+                                   "HIP events around graph replays of 20 launches; launch-bound",
+                         "avg_call_us": res["update_us"]},
+            "drop_in_refill_us_per_step": res["drop_in_us"],
+            "detail": res,
+        }
+        if res["reference_us"] is not None:
+            result["cpu_baseline"] = {"value": res["reference_us"], "unit": "us/step", "cores": 1, "kind": "port",
+                                      "sample": "16 decode steps of the reference's element-by-element refill "
+                                                "(oracle restatement of engine/kv_cache.py:147-151 and "
+                                                "engine/executor.py:345-356) on device tensors, median of 3"}
         print(json.dumps(result), flush=True)
         return 0
     print(f"[bench] building {args.workload} workload (seed={args.seed})", file=sys.stderr, flush=True)

@@ -7,7 +7,12 @@
  *     engine/executor.py:119-120, :151-153, :260-261, :385-386 and
  *     engine/speculative_executor.py:150-153 (append + paged attention in one call);
  *   - the per-page torch copy_ loop of FlashAttnKVCache.transfer_sequence
- *     (engine/kv_cache.py:189-207), generalised to copy-on-write and compaction.
+ *     (engine/kv_cache.py:189-207), generalised to copy-on-write and compaction;
+ *   - the elementwise steps on either side of attention (QKV split + QK-norm + RoPE with the
+ *     paged append, RMSNorm with the residual add, SiLU-mul: engine/executor.py,
+ *     engine/fused_kernels.py);
+ *   - the per-step refill of a graph-captured decode batch's block table and lengths
+ *     (engine/kv_cache.py:147-151, engine/executor.py:345-353), as incremental updates.
  *
  * Conventions shared by every entry point:
  *   - All tensors are device pointers owned by the caller.  Nothing here allocates device
@@ -216,6 +221,20 @@ int pkv_rms_norm(const void* x, int64_t x_stride, const void* residual, int64_t 
  */
 int pkv_silu_mul(const void* gate, int64_t g_stride, const void* up, int64_t u_stride,
                  void* out, int64_t o_stride, int64_t rows, int32_t m, void* stream);
+
+/*
+ * Incremental update of a device-resident decode block table and its cache_seqlens (replaces the
+ * per-step refill of the reference's graph buffers: engine/kv_cache.py:147-151 writes every
+ * block_table[i, j] and cache_seqlens[i] of the batch element by element, then
+ * engine/executor.py:345-353 zeroes and copies the graph's static bt / sl).  packet (device
+ * int32) holds n_len (row, length) pairs, then n_ent (row, column, page) triples:
+ *   cache_seqlens[row] = length;   block_table[row * bt_stride + column] = page.
+ * Entries outside rows x cols, negative lengths and pages outside [0, num_pages) are skipped and
+ * flag PKV_STATUS_BAD_PAGE in *status.  One launch; asynchronous on `stream`.
+ */
+int pkv_table_update(const int32_t* packet, int32_t n_len, int32_t n_ent, int32_t* block_table,
+                     int64_t bt_stride, int32_t* cache_seqlens, int32_t rows, int32_t cols,
+                     int32_t num_pages, int32_t* status, void* stream);
 
 #ifdef __cplusplus
 }

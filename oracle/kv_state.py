@@ -13,6 +13,8 @@ the product tests then check separately):
     IndexError (:79, :82); _ensure_capacity raises RuntimeError when out of pages (:120);
   * free_all resets the free list to [max_pages-1, ..., 0] (:99-103);
   * build_block_table rows hold each sequence's page list (:147-151), cache_seqlens = seq_len;
+    graph_staging_elementwise restates that loop plus the executor's refill of a captured
+    batch's static buffers (engine/executor.py:345-356), element by element;
   * transfer_sequence copies ceil(seq_len / P) pages after new_sequence + _ensure_capacity on the
     target (:183-207);
   * PrefixCache: only full page_size blocks are hashed (:41-45, :77); the key chains
@@ -115,6 +117,36 @@ class KVAllocatorRef:
         target._ensure_capacity(dst, src_len)
         target.seq_len[dst] = src_len
         return n, list(zip(self.seq_pages[seq_id][:n], target.seq_pages[dst][:n]))
+
+
+def graph_staging_elementwise(bt, sl, graph_bt, graph_sl, seq_pages, seq_len, seq_ids,
+                              cos=None, sin=None, graph_cos=None, graph_sin=None):
+    """The reference's per-step refill of a captured decode batch's inputs, one element at a time
+    on whatever tensors are passed (device tensors on the GPU box, so each write is its own
+    host-to-device copy, as in the reference):
+
+      build_block_table (engine/kv_cache.py:147-151): bt[i, j] = page; sl[i] = seq_len[sid]
+      batched_decode_step (engine/executor.py:345-356): graph_bt[:] = 0; graph_bt[:B, :nb] = bt;
+          graph_sl[:] = 0; graph_sl[:B] = sl; graph_cos[i, 0] = cos[pos_i]; graph_sin[i, 0] = sin[pos_i]
+
+    bt / sl are the persistent build buffers (at least [B, max pages] / [B]); cos / sin are
+    [n_pos, hd] tables and graph_cos / graph_sin [rows, 1, hd] (optional).  Timed as the
+    reference-side cost of DecodeBatch.step; tests pin the resulting rows against block_table().
+    """
+    B = len(seq_ids)
+    nb = max(1, max(len(seq_pages[s]) for s in seq_ids)) if seq_ids else 1
+    for i, sid in enumerate(seq_ids):
+        for j, page in enumerate(seq_pages[sid]):
+            bt[i, j] = page
+        sl[i] = seq_len[sid]
+    graph_bt[:] = 0
+    graph_bt[:B, :nb] = bt[:B, :nb]
+    graph_sl[:] = 0
+    graph_sl[:B] = sl[:B]
+    if cos is not None:
+        for i, sid in enumerate(seq_ids):
+            graph_cos[i, 0].copy_(cos[seq_len[sid]])
+            graph_sin[i, 0].copy_(sin[seq_len[sid]])
 
 
 class PrefixCacheRef:

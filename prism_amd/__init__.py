@@ -3,11 +3,14 @@
 Drop-ins for Prism's engine/kv_cache.py (FlashAttnKVCache), engine/prefix_cache.py
 (PrefixCache), the flash_attn.flash_attn_with_kvcache op it calls and the elementwise steps on
 either side of it (QKV split + RoPE, RMSNorm, SiLU-mul; engine/executor.py,
-engine/fused_kernels.py), backed by hand-written gfx950 HIP kernels in libprism_kv.so (C ABI:
-include/prism_kv.h).  There is no CPU path: device ops raise if the library is not built.
+engine/fused_kernels.py) and a device-resident block table for graph-captured decode batches
+(DecodeBatch, replacing the per-step refill of engine/executor.py:320-356), backed by
+hand-written gfx950 HIP kernels in libprism_kv.so (C ABI: include/prism_kv.h).  There is no
+CPU path: device ops raise if the library is not built.
 """
 from .attention import (append_kv, decode_attention, flash_attn_with_kvcache, prefill_attention,
                         read_status, status_tensor)
+from .decode_batch import DecodeBatch
 from .epilogue import fused_rms_norm, fused_silu_mul, rms_norm, rope_qk, rope_tables, silu_mul
 from .kv_cache import FlashAttnKVCache, KVCacheOutOfPages, copy_pages
 from .prefix_cache import CachedPrefix, PrefixCache
@@ -17,4 +20,5 @@ __all__ = [
     "flash_attn_with_kvcache", "append_kv", "decode_attention", "prefill_attention",
     "copy_pages", "read_status", "status_tensor",
     "rope_tables", "rope_qk", "rms_norm", "fused_rms_norm", "silu_mul", "fused_silu_mul",
+    "DecodeBatch",
 ]

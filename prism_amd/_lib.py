@@ -100,6 +100,7 @@ _SIGNATURES = {
         _I64, _I32, c_float, _P,         # rows, hidden, eps, stream
     ]),
     "pkv_silu_mul": (c_int32, [_P, _I64, _P, _I64, _P, _I64, _I64, _I32, _P]),
+    "pkv_table_update": (c_int32, [_P, _I32, _I32, _P, _I64, _P, _I32, _I32, _I32, _P, _P]),
 }
 
 _lock = threading.Lock()

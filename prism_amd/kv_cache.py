@@ -69,6 +69,7 @@ class FlashAttnKVCache:
         self._holders: dict[int, int] = {}     # page -> number of live sequences listing it
         self.prefix_cache = None               # set by PrefixCache(kv)
         self._bases: torch.Tensor | None = None
+        self.null_page: int | None = None      # reserve_null_page()
 
         self._max_blocks_per_seq = 32
         self._block_table_buf = torch.zeros(1, self._max_blocks_per_seq, dtype=torch.int32, device=device)
@@ -92,6 +93,21 @@ class FlashAttnKVCache:
         if not self.free_pages:
             raise KVCacheOutOfPages(f"Out of KV cache pages ({self.max_pages} total)")
         return self.free_pages.pop()
+
+    def _all_pages_free(self) -> list[int]:
+        return [p for p in range(self.max_pages - 1, -1, -1) if p != self.null_page]
+
+    def reserve_null_page(self) -> int:
+        """Take one page off the free list for good and return its id (the same id on every call).
+
+        Padded rows of a graph-captured batch point their block table at it, so the dummy K/V
+        their append writes never lands in a page a sequence owns.  The reference points padded
+        rows at page 0 (engine/executor.py:348-353), the first page it hands out (:49).  The
+        page stays reserved through free_all; compact() reserves a fresh one in the packed pool.
+        """
+        if self.null_page is None:
+            self.null_page = self._pop_page()
+        return self.null_page
 
     def _hold(self, page: int) -> None:
         self._holders[page] = self._holders.get(page, 0) + 1
@@ -157,7 +173,7 @@ class FlashAttnKVCache:
             self.free_sequence(sid)
 
     def free_all(self) -> None:
-        self.free_pages = list(range(self.max_pages - 1, -1, -1))
+        self.free_pages = self._all_pages_free()
         self.seq_pages.clear()
         self.seq_len.clear()
         self.seq_owner.clear()
@@ -311,11 +327,11 @@ class FlashAttnKVCache:
         if (target.num_layers, target.num_kv_heads, target.head_dim, target.page_size, target.dtype) != \
                 (self.num_layers, self.num_kv_heads, self.head_dim, self.page_size, self.dtype):
             raise RuntimeError("migrate_to needs a target cache of the same geometry")
-        if target.seq_pages or target.pages_used:
+        if target.seq_pages or target.pages_used > (target.null_page is not None):
             raise RuntimeError("migrate_to needs an empty target cache")
         live = self.live_pages()
-        if len(live) > target.max_pages:
-            raise KVCacheOutOfPages(f"{len(live)} live pages do not fit {target.max_pages}")
+        if len(live) > target.pages_free:
+            raise KVCacheOutOfPages(f"{len(live)} live pages do not fit {target.pages_free}")
         remap = {p: target._pop_page() for p in live}
         if live:
             copy_pages(self, target, live, [remap[p] for p in live], None)
@@ -332,7 +348,7 @@ class FlashAttnKVCache:
             pc.kv = target
             target.prefix_cache = pc
             self.prefix_cache = None
-        self.free_pages = list(range(self.max_pages - 1, -1, -1))
+        self.free_pages = self._all_pages_free()
         self.seq_pages.clear()
         self.seq_len.clear()
         self.seq_owner.clear()
@@ -358,6 +374,9 @@ class FlashAttnKVCache:
         if fresh.prefix_cache is not None:
             fresh.prefix_cache.kv = self
             self.prefix_cache = fresh.prefix_cache
+        if self.null_page is not None:
+            self.null_page = None
+            self.reserve_null_page()
         return remap
 
 
