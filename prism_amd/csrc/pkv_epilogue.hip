@@ -188,6 +188,13 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const NormParams p) {
   const int r = blockIdx.x;
   const int nch = p.hidden / 8;
   const uint16_t* x = p.x + r * p.x_stride;
+  // the weight chunks go out with the row's loads: they are independent of the sum of squares
+  u32x4 wv[kNormMaxChunks];
+#pragma unroll
+  for (int k = 0; k < kNormMaxChunks; ++k) {
+    const int c = threadIdx.x + 256 * k;
+    if (c < nch) wv[k] = ld16(p.w + 8 * c);
+  }
   u32x4 hv[kNormMaxChunks];
   float ss = 0.f;
 #pragma unroll
@@ -224,7 +231,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const NormParams p) {
     if (c < nch) {
       float f[8], w[8];
       unpack8(hv[k], f);
-      unpack8(ld16(p.w + 8 * c), w);
+      unpack8(wv[k], w);
 #pragma unroll
       for (int e = 0; e < 8; ++e) f[e] = f[e] * rs * w[e];
       st16(p.out + r * p.o_stride + 8 * c, pack8(f));
