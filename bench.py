@@ -194,6 +194,17 @@ def config5_page_ops(prism_amd, w, dev) -> dict:
     nbytes = 2 * len(live) * kv.bytes_per_page * 2 * L
     out["compaction"] = {"pages": len(live), "us": round(ms * 1e3, 1), "bytes": nbytes,
                          "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    # the disaggregated transfer path on one device: one child's pages (every layer, K and V)
+    # gathered into staging, copied once as a block (the xGMI peer copy between GPUs), scattered
+    # into another cache; bytes = the pages' bytes once (what a transfer moves)
+    sid = w.seq_ids[-1]
+    n = -(-kv.seq_len[sid] // kv.page_size)
+    pages = kv.seq_pages[sid][:n]
+    target = prism_amd.FlashAttnKVCache(L, kv.num_kv_heads, kv.head_dim, n, kv.page_size, str(dev))
+    ms = time_eager(lambda: prism_amd.copy_pages(kv, target, pages, list(range(n)), None, staged=True), 5)
+    nbytes = 2 * n * kv.bytes_per_page * L
+    out["staged_transfer"] = {"pages": n, "tokens": kv.seq_len[sid], "us": round(ms * 1e3, 1), "bytes": nbytes,
+                              "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
     return out
 
 

@@ -292,8 +292,9 @@ class FlashAttnKVCache:
         return self._bases
 
     def transfer_sequence(self, seq_id: int, target_kv: "FlashAttnKVCache",
-                          target_seq_id: int | None = None) -> int:
-        """Copy a sequence's KV into another cache (engine/kv_cache.py:174-209); returns #pages."""
+                          target_seq_id: int | None = None, staged: bool | None = None) -> int:
+        """Copy a sequence's KV into another cache (engine/kv_cache.py:174-209); returns #pages.
+        staged: see copy_pages (the default stages only between devices)."""
         if seq_id not in self.seq_pages:
             return 0
         dst_seq_id = target_seq_id if target_seq_id is not None else seq_id
@@ -304,7 +305,7 @@ class FlashAttnKVCache:
         target_kv._ensure_capacity(dst_seq_id, src_len)
         target_kv.seq_len[dst_seq_id] = src_len
         if n:
-            copy_pages(self, target_kv, src_pages[:n], target_kv.seq_pages[dst_seq_id][:n], None)
+            copy_pages(self, target_kv, src_pages[:n], target_kv.seq_pages[dst_seq_id][:n], None, staged)
         return n
 
     def live_pages(self) -> list[int]:
@@ -381,9 +382,14 @@ class FlashAttnKVCache:
 
 
 def copy_pages(src: FlashAttnKVCache, dst: FlashAttnKVCache, src_ids: list[int], dst_ids: list[int],
-               fill: list[int] | None) -> None:
+               fill: list[int] | None, staged: bool | None = None) -> None:
     """One pkv_copy_pages launch over every layer's K and V: dst[dst_ids[i]] <- src[src_ids[i]]
-    (first fill[i] slots, or whole pages), asynchronous on the current stream."""
+    (first fill[i] slots, or whole pages), asynchronous on the current stream.
+
+    Between caches on different devices (or with staged=True on one device) the pages move by
+    the staged path instead: one gather of every layer's pages into a contiguous buffer on the
+    source device, one device-to-device copy of that buffer (xGMI between GPUs), one scatter
+    into the target pool."""
     if not src_ids:
         return
     if src.k_pool.device.type != "cuda" or dst.k_pool.device.type != "cuda":
@@ -391,8 +397,8 @@ def copy_pages(src: FlashAttnKVCache, dst: FlashAttnKVCache, src_ids: list[int],
                            f"{src.k_pool.device}/{dst.k_pool.device} (prism_amd has no CPU path)")
     if src.bytes_per_page != dst.bytes_per_page or src.num_layers != dst.num_layers:
         raise RuntimeError("page copy between caches of different geometry")
-    if src.k_pool.device != dst.k_pool.device:
-        _copy_pages_peer(src, dst, src_ids, dst_ids, fill)
+    if staged or (staged is None and src.k_pool.device != dst.k_pool.device):
+        _copy_pages_staged(src, dst, src_ids, dst_ids, fill)
         return
     dev = src.k_pool.device
     ids = torch.tensor([list(src_ids), list(dst_ids)] + ([list(fill)] if fill is not None else []),
@@ -408,11 +414,11 @@ def copy_pages(src: FlashAttnKVCache, dst: FlashAttnKVCache, src_ids: list[int],
     _lib.check(rc, "pkv_copy_pages")
 
 
-def _copy_pages_peer(src: FlashAttnKVCache, dst: FlashAttnKVCache, src_ids, dst_ids, fill) -> None:
-    """Cross-device move: gather on the source GPU, one peer copy (xGMI), scatter on the target.
-
-    Needs two GPUs; not exercised on a one-GPU host.
-    """
+def _copy_pages_staged(src: FlashAttnKVCache, dst: FlashAttnKVCache, src_ids, dst_ids, fill) -> None:
+    """Disaggregated move (engine/kv_cache.py:174-209 transfer_sequence, engine/disaggregated.py:144):
+    gather on the source device into [2L, n, page] staging, one copy of the staging buffer to the
+    target device (a peer copy over xGMI between GPUs; the same code on one device), scatter into
+    the target pool.  Three launches for any number of layers and pages."""
     n = len(src_ids)
     L2 = 2 * src.num_layers
     page_elems = src.page_size * src.num_kv_heads * src.head_dim

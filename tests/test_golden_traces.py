@@ -49,7 +49,7 @@ class _ProductAlloc:
 
         self.copies = []
 
-        def cpu_copy(src, dst, src_ids, dst_ids, fill):
+        def cpu_copy(src, dst, src_ids, dst_ids, fill, staged=None):
             self.copies.append((list(src_ids), list(dst_ids), fill))
             for s, d in zip(src_ids, dst_ids):
                 dst.k_pool[:, d] = src.k_pool[:, s]

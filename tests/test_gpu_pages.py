@@ -105,3 +105,36 @@ def test_compaction_preserves_every_live_page(gpu):
         assert kv.seq_pages[sid] == [remap[p] for p in pages]
     assert pc.lookup(tokens, "m") == ([remap[p] for p in owners[0][:2]], 32)
     assert kv.pages_used == len(live)
+
+
+@pytest.mark.parametrize("fill", [None, [16, 5, 1, 9]])
+def test_staged_copy_matches_direct_copy(gpu, fill):
+    # the disaggregated path (gather into staging, one device-to-device copy, scatter), forced on
+    # one device, is bit-exact with the direct copy and the oracle
+    a = _random_kv(gpu, seed=3)
+    b = _random_kv(gpu, seed=4)
+    before_a, before_b = _pools(a), _pools(b)
+    src, dst = [3, 7, 11, 19], [0, 19, 5, 12]
+    prism_amd.copy_pages(a, b, src, dst, fill, staged=True)
+    torch.cuda.synchronize()
+    expect = page_ops.copy_pages(before_a, before_b, src, dst, fill)
+    for got, exp in zip(_pools(b), expect):
+        assert np.array_equal(got, exp)
+    for got, exp in zip(_pools(a), before_a):
+        assert np.array_equal(got, exp)
+
+
+def test_staged_transfer_sequence(gpu):
+    a = _random_kv(gpu, seed=5)
+    b = _random_kv(gpu, seed=6)
+    a.new_sequence(7)
+    a._ensure_capacity(7, 40)
+    a.seq_len[7] = 40
+    src_pages = list(a.seq_pages[7])
+    before_a, before_b = _pools(a), _pools(b)
+    n = a.transfer_sequence(7, b, 9, staged=True)
+    torch.cuda.synchronize()
+    assert n == 3 and b.seq_len[9] == 40
+    expect = page_ops.transfer_sequence(before_a, before_b, src_pages, b.seq_pages[9], 40, 16)
+    for got, exp in zip(_pools(b), expect):
+        assert np.array_equal(got, exp)
