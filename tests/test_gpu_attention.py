@@ -245,3 +245,30 @@ def test_bad_page_id_is_flagged_not_faulted(gpu):
                                       cache_seqlens=dev["cache_seqlens"], block_table=bt, causal=True, status=st)
     torch.cuda.synchronize()
     assert int(st.item()) & 1
+
+
+def test_balanced_kernel_at_its_batch_limit_and_on_empty_caches(gpu):
+    # 256 sequences fill all four 64-sequence chunks of the balanced kernel's in-register scan;
+    # a batch of empty caches makes every range a run of one-tile sequences (only the new row)
+    rng = np.random.default_rng(3)
+    ctx = [int(c) for c in rng.integers(0, 120, size=256)]
+    _run_and_check(gpu, batch=256, ctx=ctx, page_size=32, n_kv=4, n_heads=28, head_dim=128, s_q=1,
+                   what="balanced B=256")
+    _run_and_check(gpu, batch=256, ctx=ctx, page_size=32, n_kv=4, n_heads=28, head_dim=128, s_q=2,
+                   what="balanced B=256 verify")
+    _run_and_check(gpu, batch=8, ctx=[0] * 8, page_size=256, n_kv=4, n_heads=28, head_dim=128, s_q=1,
+                   what="all empty")
+
+
+@pytest.mark.parametrize("batch,ctx,s_q", [
+    (64, [(i * 37) % 300 for i in range(64)], 8),   # the largest batch ranked by length
+    (6, [200, 200, 200, 35, 200, 0], 24),           # equal lengths: ties ranked by index
+    (70, [(i * 53) % 260 for i in range(70)], 4),   # above 64 sequences: launch order
+])
+def test_prefill_launch_order_covers_every_item(gpu, batch, ctx, s_q):
+    # the prefill grid is walked heaviest first; every (sequence, KV head, row block) item must
+    # still be computed exactly once (the NaN-filled output catches a missed one)
+    _run_and_check(gpu, batch=batch, ctx=ctx, page_size=32, n_kv=4, n_heads=28, head_dim=128, s_q=s_q,
+                   kernel="prefill", what=f"prefill order B={batch}")
+    _run_and_check(gpu, batch=batch, ctx=ctx, page_size=16, n_kv=2, n_heads=14, head_dim=64, s_q=s_q,
+                   kernel="prefill", what=f"prefill order hd64 B={batch}")
