@@ -600,6 +600,53 @@ def main() -> int:
         cfg["workload"] = ("config5: Qwen2.5-7B shared 2048-token prefix (ref-counted, copy-on-write boundary "
                            "page) + speculative verify of 5 draft tokens, 28 layers, b=64, suffix ~U{0..1024}")
         cfg.update({k: v for k, v in w.meta.items() if k != "shape"})
+        # cascade attention over the pages every child shares (the full pages of the prefix; the
+        # boundary page was copied into each child): the prefix read once per layer for the batch
+        shared_tokens = (w.meta["shared_prefix"] // kv.page_size) * kv.page_size
+
+        def cascade_step():
+            for l in range(L):
+                prism_amd.flash_attn_with_kvcache(w.q[l], kv.k_caches[l], kv.v_caches[l], k=w.k[l], v=w.v[l],
+                                                  cache_seqlens=w.cache_seqlens, block_table=w.block_table,
+                                                  causal=True, out=outs[l], shared_prefix_tokens=shared_tokens)
+
+        cascade_ms = time_graph(cascade_step, args, dev)
+        c_status = prism_amd.read_status(dev)
+        if c_status:
+            print(f"[bench] WARNING: cascade status flags {c_status}", file=sys.stderr)
+        c_us = cascade_ms * 1e3 / L
+        unique_layer = bytes_layer - (w.batch - 1) * shared_tokens * kv.num_kv_heads * kv.head_dim * 2 * 2
+        print(f"[bench] cascade: call avg {c_us:.2f} us ({shared_tokens} shared tokens)", file=sys.stderr, flush=True)
+        cascade = {"shared_tokens": shared_tokens, "avg_call_us": round(c_us, 3), "ms_per_step": round(cascade_ms, 4),
+                   "speedup": round(call_us / c_us, 3), "unique_bytes_per_call": unique_layer,
+                   "gbs_unique": round(unique_layer / (c_us * 1e-6) / 1e9, 1),
+                   "frac_unique": round(unique_layer / (c_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                   "mfma_tflops": round(flops_layer / (c_us * 1e-6) / 1e12, 2),
+                   "mfma_frac": round(flops_layer / (c_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                   "kernels": "prefill_lds_kernel (prefix pass, key splits) + decode_lean_kernel<3> (suffixes) + "
+                              "combine_lean_kernel; HIP events around graph replays"}
+        # the same verify where the shared prefix dominates (8192-token prompt, suffixes <= 256)
+        wl = workloads.config5(dev, seed=args.seed, prefix=8192, max_suffix=256)
+        shared_l = (wl.meta["shared_prefix"] // wl.kv.page_size) * wl.kv.page_size
+        outs_l = [torch.empty_like(q) for q in wl.q]
+
+        def long_step(sp):
+            def f():
+                for l in range(wl.layers):
+                    prism_amd.flash_attn_with_kvcache(wl.q[l], wl.kv.k_caches[l], wl.kv.v_caches[l], k=wl.k[l],
+                                                      v=wl.v[l], cache_seqlens=wl.cache_seqlens,
+                                                      block_table=wl.block_table, causal=True, out=outs_l[l],
+                                                      shared_prefix_tokens=sp)
+            return f
+
+        plain_l = time_graph(long_step(0), args, dev) * 1e3 / wl.layers
+        casc_l = time_graph(long_step(shared_l), args, dev) * 1e3 / wl.layers
+        print(f"[bench] long prefix: plain {plain_l:.2f} us, cascade {casc_l:.2f} us", file=sys.stderr, flush=True)
+        cascade["long_prefix"] = {"prefix": 8192, "max_suffix": 256, "shared_tokens": shared_l,
+                                  "plain_us": round(plain_l, 3), "cascade_us": round(casc_l, 3),
+                                  "speedup": round(plain_l / casc_l, 3)}
+        del wl, outs_l
+        torch.cuda.empty_cache()
         page_ops = config5_page_ops(prism_amd, w, dev)
         result = {
             "metric": "speculative verify attn HBM GB/s (% of peak) + MFMA %, Qwen2.5-7B shape b=64 draft 5",
@@ -615,6 +662,7 @@ def main() -> int:
                 "bytes_per_call": bytes_layer, "flops_per_call": flops_layer, "avg_call_us": round(call_us, 3),
             },
             "page_ops": page_ops,
+            "cascade": cascade,
         }
         unit = "GB/s"
     if not args.no_cpu_baseline:

@@ -51,6 +51,8 @@ extern "C" {
 
 #define PKV_STATUS_BAD_PAGE 1
 #define PKV_STATUS_BAD_POSITION 2  /* a rotary position outside the cos/sin table (clamped) */
+#define PKV_STATUS_SHARED_PREFIX 4 /* pkv_cascade_attn: a sequence shorter than the shared prefix
+                                      or not listing its pages */
 
 /* pkv_decode_attn flags (0 = the library's choice of kernel and merge) */
 #define PKV_DECODE_TWO_PASS 1    /* merge split-K partials in a second launch */
@@ -128,6 +130,35 @@ int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
                     int32_t page_size, int32_t num_pages, int32_t max_blocks,
                     int32_t causal, float softmax_scale, int32_t split_tokens, int32_t flags,
                     int32_t* status, void* stream);
+
+/*
+ * Cascade (shared-prefix) attention: pkv_decode_attn for a batch whose sequences all list the
+ * same pages for their first shared_tokens keys (branches of one prompt: the speculative verify
+ * of engine/speculative_executor.py:113-164 over a cached prefix, engine/prefix_cache.py).
+ * Same arguments and results as pkv_decode_attn (flags 0), plus shared_tokens: a multiple of
+ * page_size, every sequence holding at least shared_tokens keys before the append.  The prefix
+ * is read once for the whole batch (every query row against it, in key splits, on MFMA), the
+ * rest of each sequence by the balanced decode kernel, and one launch merges both.  A sequence
+ * shorter than the prefix or not listing sequence 0's prefix pages sets
+ * PKV_STATUS_SHARED_PREFIX (its output is then meaningless; every access stays in the pool).
+ * Shapes outside the balanced kernel's (see pkv_decode_attn) and shared_tokens = 0 run
+ * pkv_decode_attn.  workspace: pkv_cascade_workspace_bytes() bytes, same rules as
+ * pkv_decode_attn's.
+ */
+size_t pkv_cascade_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv,
+                                   int32_t head_dim, int32_t page_size, int32_t max_blocks,
+                                   int32_t shared_tokens);
+
+int pkv_cascade_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                     const void* k_new, int64_t kn_sb, int64_t kn_ss, int64_t kn_sh,
+                     const void* v_new, int64_t vn_sb, int64_t vn_ss, int64_t vn_sh,
+                     void* k_cache, void* v_cache, int64_t cache_page_stride,
+                     const int32_t* block_table, int64_t bt_stride, const int32_t* cache_seqlens,
+                     void* out, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+                     void* workspace, size_t workspace_bytes,
+                     int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv, int32_t head_dim,
+                     int32_t page_size, int32_t num_pages, int32_t max_blocks, int32_t shared_tokens,
+                     int32_t causal, float softmax_scale, int32_t* status, void* stream);
 
 /*
  * Varlen chunked-prefill attention over paged KV (flash_attn_with_kvcache with s_q = chunk,

@@ -20,6 +20,7 @@ PKV_EHIP = -2
 PKV_ENOSPC = -3
 PKV_STATUS_BAD_PAGE = 1
 PKV_STATUS_BAD_POSITION = 2
+PKV_STATUS_SHARED_PREFIX = 4
 PKV_DECODE_TWO_PASS = 1
 PKV_DECODE_FUSED_MERGE = 2
 PKV_DECODE_HEADS = 4
@@ -101,6 +102,10 @@ _SIGNATURES = {
     ]),
     "pkv_silu_mul": (c_int32, [_P, _I64, _P, _I64, _P, _I64, _I64, _I32, _P]),
     "pkv_table_update": (c_int32, [_P, _I32, _I32, _P, _I64, _P, _I32, _I32, _I32, _P, _P]),
+    "pkv_cascade_workspace_bytes": (c_size_t, [_I32] * 8),
+    "pkv_cascade_attn": (c_int32, [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64,
+                                   _P, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _P, c_size_t,
+                                   _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, c_float, _P, _P]),
 }
 
 _lock = threading.Lock()

@@ -179,6 +179,7 @@ def flash_attn_with_kvcache(
     two_pass: bool | None = None,
     kernel: str = "auto",
     grid: int = 0,
+    shared_prefix_tokens: int = 0,
     status: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Append k/v into the paged cache and attend (see module docstring for the contract).
@@ -191,6 +192,13 @@ def flash_attn_with_kvcache(
     to finish its part of a sequence), None lets the library choose (a second launch for the
     balanced kernel, in-launch for the per-head kernel).  ``kernel="heads"`` forces the per-head kernel where the balanced one would
     run; ``grid`` > 0 runs the balanced kernel on that many workgroups instead of one per CU.
+
+    ``shared_prefix_tokens`` > 0 (a multiple of the page size) declares that every sequence of
+    the batch lists the same pages for its first shared_prefix_tokens keys and holds at least
+    that many keys before the append (branches of one prompt, e.g. a speculative verify batch):
+    cascade attention then reads that prefix once for the whole batch (pkv_cascade_attn).
+    A sequence that breaks the promise sets PKV_STATUS_SHARED_PREFIX in the status word.
+    Shapes the cascade does not cover run the ordinary decode path.
     """
     if rotary_cos is not None or rotary_sin is not None or cache_batch_idx is not None \
             or cache_leftpad is not None or tuple(window_size) != (-1, -1) or softcap != 0.0 \
@@ -252,6 +260,20 @@ def flash_attn_with_kvcache(
         if num_splits and num_splits > 0 and not split_tokens:
             per_split = -(-(max_blocks * page_size) // num_splits)
             split_tokens = max(32, -(-per_split // 32) * 32)
+        if shared_prefix_tokens and not split_tokens and kernel == "auto" and not grid and two_pass is not False:
+            nbytes = lib.pkv_cascade_workspace_bytes(batch, s_q, n_heads, n_kv, hd, page_size, max_blocks,
+                                                     int(shared_prefix_tokens))
+            ws = _workspace(device, nbytes, stream)
+            rc = lib.pkv_cascade_attn(
+                q.data_ptr(), *qs, kp, *ks, vp, *vs,
+                k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
+                block_table.data_ptr(), block_table.stride(0), cache_seqlens.data_ptr(),
+                out.data_ptr(), *os_,
+                ws.data_ptr() if ws is not None else 0, ws.numel() if ws is not None else 0,
+                batch, s_q, n_heads, n_kv, hd, page_size, num_pages, max_blocks, int(shared_prefix_tokens),
+                1 if causal else 0, scale, st.data_ptr(), stream)
+            _lib.check(rc, "pkv_cascade_attn")
+            return out
         nbytes = lib.pkv_decode_workspace_bytes(batch, s_q, n_heads, n_kv, hd, page_size, max_blocks,
                                                 int(split_tokens))
         ws = _workspace(device, nbytes, stream)

@@ -49,6 +49,12 @@ struct AttnParams {
   int batch, s_q, g, R, n_kv, log2_page, num_pages, max_blocks, split_tokens, max_splits;
   int causal, has_new, two_pass;
   int lean_grid;  // workgroups of a decode_lean_kernel launch (its combine needs the same split)
+  // Cascade (shared-prefix) attention: the first k0 keys of every sequence are the same pages
+  // (k0 a multiple of the page size).  cascade_splits > 0 turns it on: the prefix pass writes
+  // cascade_splits partials per sequence (slots 2 G + b S + s), decode_lean_kernel covers keys
+  // [k0, L) and writes every segment as a partial (whole sequences to slot 2 G + B S + b), and
+  // the combine merges them all.  k0 = 0 and cascade_splits = 0 otherwise.
+  int k0, cascade_splits;
   float scale_log2;  // softmax_scale * log2(e)
 };
 
@@ -232,6 +238,34 @@ __device__ __forceinline__ void load_q(const AttnParams& p, const SeqView& sv, i
       for (int kk = 0; kk < HD / 32; ++kk) qf[nt][kk] = __builtin_bit_cast(bf16x8, ld16(base + 32 * kk));
       const int last = p.causal ? (L - p.s_q + j) : (L - 1);
       lim[nt] = min(last, sv.t_end - 1);
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < HD / 32; ++kk) qf[nt][kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+      lim[nt] = -1;
+    }
+  }
+}
+
+// load_q for the cascade prefix pass: rows r < batch * R of the whole batch (sequence r / R,
+// row r % R of it), every one seeing keys [0, last_key].
+template <int HD, int NT>
+__device__ __forceinline__ void load_q_batch_rows(const AttnParams& p, int h, int row0, int last_key,
+                                                  bf16x8 (&qf)[NT][HD / 32], int (&lim)[NT]) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15;
+  const int lq = lane >> 4;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int ra = row0 + li + 16 * nt;
+    if (ra < p.batch * p.R) {
+      const int b = ra / p.R;
+      const int rr = ra - b * p.R;
+      const int j = rr / p.g;
+      const int hq = rr - j * p.g;
+      const uint16_t* base = p.q + b * p.q_sb + j * p.q_ss + (h * p.g + hq) * p.q_sh + 8 * lq;
+#pragma unroll
+      for (int kk = 0; kk < HD / 32; ++kk) qf[nt][kk] = __builtin_bit_cast(bf16x8, ld16(base + 32 * kk));
+      lim[nt] = last_key;
     } else {
 #pragma unroll
       for (int kk = 0; kk < HD / 32; ++kk) qf[nt][kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
@@ -887,6 +921,13 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
 
 __device__ __forceinline__ int tiles_of(int L) { return L > 0 ? (L + rows::TILE - 1) / rows::TILE : 1; }
 
+// Tiles of a sequence of L keys in a balanced launch: keys [k0, L) (k0 tile-aligned), at least one
+// (a sequence without keys there still yields its zero output or empty partial).
+__device__ __forceinline__ int seq_tiles(const AttnParams& p, int L) {
+  const int t = tiles_of(L) - p.k0 / rows::TILE;
+  return t > 0 ? t : 1;
+}
+
 // Every sequence's clamped lengths and first tile, 64 sequences per register (lane l of register
 // q holds sequence 64q + l), from one read of cache_seqlens per wave.  The clamp is seq_lengths'.
 struct SeqTable {
@@ -917,7 +958,7 @@ __device__ __forceinline__ void seq_table(const AttnParams& p, SeqTable& st) {
       c = min(max(c, 0), cap);
       L = min(c + s_new, cap);
     }
-    const int n = b < p.batch ? tiles_of(L) : 0;
+    const int n = b < p.batch ? seq_tiles(p, L) : 0;
     const int incl = base + wave_incl_scan(n);
     st.c[q] = c;
     st.L[q] = L;
@@ -975,7 +1016,7 @@ __device__ __forceinline__ void tile_window(const AttnParams& p, const SeqTable&
   int b, first, c, L;
   locate_tile(p, st, x, b, first, c, L);
   b = min(b, p.batch - 1);
-  const int T0 = (x - first) * rows::TILE;
+  const int T0 = (x - first) * rows::TILE + p.k0;
   const int col = T0 >> p.log2_page;
   const int pid = unsigned(col) < unsigned(p.max_blocks) ? p.block_table[int64_t(b) * p.bt_stride + col] : -1;
   const bool ok = unsigned(pid) < unsigned(p.num_pages);
@@ -1187,7 +1228,7 @@ struct SeqParts {
   int np, w0, slot0;
 };
 
-__device__ __forceinline__ SeqParts seq_parts(const SeqTable& st, int b, int per) {
+__device__ __forceinline__ SeqParts seq_parts(const AttnParams& p, const SeqTable& st, int b, int per) {
   int first = 0, L = 0;
 #pragma unroll
   for (int q = 0; q < rows::kChunks; ++q) {
@@ -1198,7 +1239,7 @@ __device__ __forceinline__ SeqParts seq_parts(const SeqTable& st, int b, int per
   }
   SeqParts sp;
   sp.w0 = first / per;
-  sp.np = (first + tiles_of(L) - 1) / per - sp.w0 + 1;
+  sp.np = (first + seq_tiles(p, L) - 1) / per - sp.w0 + 1;
   sp.slot0 = 2 * sp.w0 + (first != sp.w0 * per ? 1 : 0);
   return sp;
 }
@@ -1362,7 +1403,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   rows_issue<kPolicy>(p, dA, kQInLds, lds);
   if (n > 1) {
     dB = tile_desc(win, s + 1);
-    rows_issue<kPolicy>(p, dB, kQInLds && dB.T0 == 0, lds + BUF);
+    rows_issue<kPolicy>(p, dB, kQInLds && dB.T0 == p.k0, lds + BUF);
   }
 
   bf16x8 qf[NT][HD / 32];
@@ -1394,9 +1435,9 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     if (j + 1 >= n)
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     else
-      wait_vmcnt_at_most((kQInLds && dB.T0 == 0 ? 20 : 16) + stores_prev + stores_prev2);
+      wait_vmcnt_at_most((kQInLds && dB.T0 == p.k0 ? 20 : 16) + stores_prev + stores_prev2);
     raw_barrier();  // ... and every other wave's
-    if (j == 0 || d.T0 == 0) {
+    if (j == 0 || d.T0 == p.k0) {
       // a segment starts: its Q operand, row limits and a fresh softmax state
       if constexpr (kQInLds)
         rows_read_q(p, buf, h, qf);
@@ -1451,14 +1492,17 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
       else
         compute_tile<HD, NT, true>(p, tl, d.T0, qf, lim, lim_min, m_run, l_run, acc);
     }
-    if (next2) rows_issue<kPolicy>(p, d2, kQInLds && d2.T0 == 0, buf, 4, 8);
+    if (next2) rows_issue<kPolicy>(p, d2, kQInLds && d2.T0 == p.k0, buf, 4, 8);
 
     stores_prev2 = stores_prev;
     stores_prev = 0;
     if (j + 1 < n && d.T0 + rows::TILE < d.L) continue;  // the segment goes on
     // ---- segment epilogue: wave h owns head h's rows li + 16 nt < R (per N tile 4 stores, or
     // 4 + 1 for a partial; every N tile has a real row) ----
-    const bool whole = seg_T0 == 0 && d.T0 + rows::TILE >= d.L;
+    // a segment holding the sequence's keys [k0, L) complete: its final output, or in a cascade
+    // launch its suffix partial (one slot per sequence: a range may hold several)
+    const bool complete = seg_T0 == p.k0 && d.T0 + rows::TILE >= d.L;
+    const bool whole = complete && !p.cascade_splits;
     stores_prev = (whole ? 4 : 5) * NT;
     float lsum[NT];
 #pragma unroll
@@ -1486,8 +1530,11 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
       // part of a sequence shared with a neighbouring range: unnormalised partial (device-
       // coherent stores), merged at the end of the launch by the last range to finish its part,
       // or by the combine launch (two-pass)
-      const int slot = 2 * int(blockIdx.x) + (seg_j0 == 0 ? 0 : 1);
-      if (seg_j0 == 0)
+      const int slot = complete ? 2 * p.lean_grid + p.batch * p.cascade_splits + d.b
+                                : 2 * int(blockIdx.x) + (seg_j0 == 0 ? 0 : 1);
+      if (complete)
+        ;
+      else if (seg_j0 == 0)
         pub_first = d.b;
       else
         pub_last = d.b;
@@ -1537,7 +1584,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   for (int k = 0; k < 2; ++k) {
     const int b = k == 0 ? pub_first : pub_last;
     if (b < 0) continue;
-    const SeqParts sp = seq_parts(st, b, per);
+    const SeqParts sp = seq_parts(p, st, b, per);
     if ((k == 0 ? prev0 : prev1) != sp.np - 1) continue;
     if (lane == 0) __hip_atomic_store(p.ws_cnt + b * rows::NKV + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     merge_parts_for<NT>(p, b, h, sp, area, 2 * BUF / rows::NKV);
@@ -1589,20 +1636,29 @@ __global__ __launch_bounds__(1024) void combine_lean_kernel(const AttnParams p, 
     }
   }
   const int w0 = first / per;
-  const int w1 = (first + tiles_of(L) - 1) / per;
+  const int w1 = (first + seq_tiles(p, L) - 1) / per;
   const int np = w1 - w0 + 1;
-  if (np <= 1) return;
+  // cascade: the prefix pass's S parts first, then the sequence's suffix partial(s)
+  const int S = p.cascade_splits;
+  if (np <= 1 && S == 0) return;
+  const int n_parts = S + (np <= 1 ? 1 : np);
   // the first range holds b in its first segment only if b starts exactly at the range start
   const int slot0 = 2 * w0 + (first != w0 * per ? 1 : 0);
   auto row_of = [&](int part) {
-    const int slot = part == 0 ? slot0 : 2 * (w0 + part);
+    int slot;
+    if (part < S) {
+      slot = 2 * grid + b * S + part;
+    } else {
+      const int v = part - S;
+      slot = np <= 1 ? 2 * grid + p.batch * S + b : (v == 0 ? slot0 : 2 * (w0 + v));
+    }
     return (int64_t(slot) * rows::NKV + h) * p.R + r;
   };
   const uint32_t* o16 = reinterpret_cast<const uint32_t*>(p.ws_o);  // fp16 pairs
   float M_run = -INFINITY, S_run = 0.f;
   f32x2 o = {0.f, 0.f};
-  for (int u0 = 0; u0 < np; u0 += kLeanMergeBatch) {
-    const int nb = min(kLeanMergeBatch, np - u0);
+  for (int u0 = 0; u0 < n_parts; u0 += kLeanMergeBatch) {
+    const int nb = min(kLeanMergeBatch, n_parts - u0);
     uint32_t x[kLeanMergeBatch];
 #pragma unroll
     for (int k = 0; k < kLeanMergeBatch; ++k) {
@@ -1824,7 +1880,30 @@ __device__ __forceinline__ void compute_tile_prefill(const AttnParams& p, const 
       acc[nt][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[n], pb[nt], acc[nt][n], 0, 0, 0);
 }
 
-template <int NT, int W, int NBUF, int SUB>
+// Input check of a cascade launch, by one wave: sequences b0..b1 must each hold at least k0 keys
+// before the append and list sequence 0's first k0 / P pages (the prefix pass reads only those).
+// A violation flags PKV_STATUS_SHARED_PREFIX; the output of such a sequence is then meaningless,
+// but every access stays inside the pool.
+__device__ __forceinline__ void cascade_check_sharing(const AttnParams& p, int b0, int b1) {
+  if (threadIdx.x >= 64) return;
+  const int lane = threadIdx.x & 63;
+  const int np = p.k0 >> p.log2_page;
+  bool bad = false;
+  for (int b = b0; b <= b1 && b < p.batch; ++b) {
+    bad |= p.seqlens[b] < p.k0;
+    for (int c0 = 0; c0 < np; c0 += 64) {
+      const int c = c0 + lane;
+      if (c < np) bad |= p.block_table[int64_t(b) * p.bt_stride + c] != p.block_table[c];
+    }
+  }
+  if (__any(bad) && lane == 0) flag_status(p.status, PKV_STATUS_SHARED_PREFIX);
+}
+
+// CASCADE: the shared-prefix pass of a cascade launch.  Grid (row blocks of the whole batch's
+// query rows, KV heads, key splits); block-table row 0 holds the shared pages; split z covers
+// tiles [z chunk, (z + 1) chunk) of the k0 shared keys, which every row sees whole; the result is
+// a partial (fp16 O / l and fp32 log-sum-exp) in workspace slot 2 G + b S + z of each row.
+template <int NT, int W, int NBUF, int SUB, bool CASCADE = false>
 __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p) {
   constexpr int HD = pf::HD;
   constexpr int DPL = HD / 16;
@@ -1837,10 +1916,24 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
   const int li = lane & 15;
   const int lq = lane >> 4;
   int b, h, xblk;
-  prefill_item(p, b, h, xblk);
-
   int c, L;
-  seq_lengths(p, b, c, L);
+  const int R_all = CASCADE ? p.batch * p.R : p.R;  // query rows of the launch's row space
+  int t_first = 0;                                  // first tile of this workgroup's key range
+  int n_tiles;
+  if constexpr (CASCADE) {
+    xblk = blockIdx.x;
+    h = blockIdx.y;
+    b = 0;
+    c = 0;
+    L = p.k0;
+    const int n_shared = p.k0 / pf::TILE;
+    const int chunk = (n_shared + int(gridDim.z) - 1) / int(gridDim.z);
+    t_first = int(blockIdx.z) * chunk;
+    n_tiles = min(chunk, n_shared - t_first);
+  } else {
+    prefill_item(p, b, h, xblk);
+    seq_lengths(p, b, c, L);
+  }
   SeqView sv;
   sv.b = b;
   sv.h = h;
@@ -1849,17 +1942,25 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
   sv.bt = p.block_table + int64_t(b) * p.bt_stride;
 
   const int blk_row0 = xblk * W * 16 * NT;
-  if (blk_row0 >= p.R) return;
+  if (blk_row0 >= R_all) return;
   const int row0 = blk_row0 + wave * 16 * NT;
   // the block's last row sees the most keys (rows increase with j)
-  const int blk_last = min(blk_row0 + W * 16 * NT, p.R) - 1;
-  const int t_stop = p.causal ? min(L, L - p.s_q + blk_last / p.g + 1) : L;
-  const int n_tiles = t_stop > 0 ? (t_stop + pf::TILE - 1) / pf::TILE : 0;
+  const int blk_last = min(blk_row0 + W * 16 * NT, R_all) - 1;
+  if constexpr (CASCADE) {
+    if (blockIdx.z == 0 && h == 0) cascade_check_sharing(p, blk_row0 / p.R, blk_last / p.R);
+    if (n_tiles <= 0) n_tiles = 0;
+  } else {
+    const int t_stop = p.causal ? min(L, L - p.s_q + blk_last / p.g + 1) : L;
+    n_tiles = t_stop > 0 ? (t_stop + pf::TILE - 1) / pf::TILE : 0;
+  }
   const int n_stages = (n_tiles + SUB - 1) / SUB;
 
   bf16x8 qf[NT][HD / 32];
   int lim[NT];
-  load_q<HD, NT>(p, sv, L, row0, qf, lim);
+  if constexpr (CASCADE)
+    load_q_batch_rows<HD, NT>(p, h, row0, p.k0 - 1, qf, lim);
+  else
+    load_q<HD, NT>(p, sv, L, row0, qf, lim);
   int lim_min = 0x7fffffff;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) lim_min = min(lim_min, lim[nt] < 0 ? 0x7fffffff : lim[nt]);
@@ -1868,7 +1969,7 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
   lim_min = __builtin_amdgcn_readfirstlane(lim_min);
 
   BtWindow btw;
-  bt_window_load(p, sv, 0, btw);
+  bt_window_load(p, sv, (t_first * pf::TILE) >> p.log2_page, btw);
   const int row_elems = p.n_kv * HD;
   // Stage st holds tiles SUB*st .. SUB*st + SUB-1 (the last stage repeats its last real tile so
   // every stage issues the same number of copies).  Copy instruction i of a tile: K (i < 8) or V
@@ -1877,7 +1978,7 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
     char* stage = lds + (st % NBUF) * SUB * pf::BUF;
 #pragma unroll
     for (int u = 0; u < SUB; ++u) {
-      const int T0 = min(st * SUB + u, n_tiles - 1) * pf::TILE;
+      const int T0 = (t_first + min(st * SUB + u, n_tiles - 1)) * pf::TILE;
       const int pid = bt_page(p, sv, T0 >> p.log2_page, btw);
       const bool ok = unsigned(pid) < unsigned(p.num_pages);
       if (!ok && T0 < L && lane == 0) flag_status(p.status, PKV_STATUS_BAD_PAGE);
@@ -1913,7 +2014,7 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
     for (int u = 0; u < SUB; ++u) {
       const int t = st * SUB + u;
       if (t >= n_tiles) break;
-      const int T0 = t * pf::TILE;
+      const int T0 = (t_first + t) * pf::TILE;
       const char* buf = lds + ((st % NBUF) * SUB + u) * pf::BUF;
       KVTile<HD> tl;
 #pragma unroll
@@ -1939,13 +2040,39 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
           for (int w = 0; w < 4; ++w) tl.vr[e].w[w] = keep ? tl.vr[e].w[w] : 0u;
         }
       }
-      if (row0 < p.R) compute_tile_prefill<NT>(p, tl, T0, qf, lim, lim_min, m_run, l_run, acc);
+      if (row0 < R_all) compute_tile_prefill<NT>(p, tl, T0, qf, lim, lim_min, m_run, l_run, acc);
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the stage are done
     raw_barrier();                       // the stage's buffer is free
     if (st + NBUF < n_stages) issue(st + NBUF);
   }
-  if (row0 >= p.R) return;
+  if (row0 >= R_all) return;
+  if constexpr (CASCADE) {
+    // the split's partial of every row: fp16 O / l and the log-sum-exp, as the balanced kernel
+    // writes its partials
+    const uint32_t lse0 = uint32_t(p.ws_ml - p.ws_o) * 4u;
+    const __amdgpu_buffer_rsrc_t rs = ws_rsrc(p);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int ra = row0 + li + 16 * nt;
+      const float lsum = sum_over_quads(l_run[nt]);
+      if (ra < R_all) {
+        const int br = ra / p.R;
+        const int rr = ra - br * p.R;
+        const int slot = 2 * p.lean_grid + br * p.cascade_splits + int(blockIdx.z);
+        const uint32_t row = uint32_t((slot * rows::NKV + h) * p.R + rr);
+        const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+        u32x4 ov[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) ov[r][k] = pack_f16x2(acc[nt][2 * k][r] * inv, acc[nt][2 * k + 1][r] * inv);
+        const float lse = lsum > 0.f ? m_run[nt] + __builtin_amdgcn_logf(lsum) : -INFINITY;
+        ws_store_partial<0>(rs, (row * HD + 4 * DPL * lq) * 2u, ov, lq == 0, lse0 + row * 4u, lse);
+      }
+    }
+    return;
+  }
 
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
@@ -2093,6 +2220,8 @@ static void fill_params(AttnParams& p, const void* q, int64_t q_sb, int64_t q_ss
   p.has_new = k_new ? 1 : 0;
   p.two_pass = 0;
   p.lean_grid = 0;
+  p.k0 = 0;
+  p.cascade_splits = 0;
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
 }
 
@@ -2251,6 +2380,112 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
     launch_decode_hd<128>(p, batch, s);
   else
     launch_decode_hd<64>(p, batch, s);
+  return check_launch(fn);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Cascade (shared-prefix) attention: the balanced decode shapes with a prefix of shared_tokens
+// keys that every sequence of the batch holds in the same pages (speculative verify of branches
+// of one prompt, engine/speculative_executor.py:113-164).  The prefix is read once for the whole
+// batch instead of once per sequence.
+// ---------------------------------------------------------------------------------------------
+namespace pkv {
+
+static bool cascade_eligible(int batch, int head_dim, int n_kv, int R, int page_size, int max_blocks,
+                             int shared_tokens) {
+  return use_lean_kernel(batch, head_dim, n_kv, R, page_size, 0, 0) && shared_tokens > 0 &&
+         shared_tokens % page_size == 0 && int64_t(shared_tokens) <= int64_t(max_blocks) * page_size;
+}
+
+// Key splits of the prefix pass: as many as keep (row blocks of 128 rows x KV heads x splits)
+// within one round of two workgroups per CU, at least two 32-token tiles per split.
+static int cascade_splits_for(int batch, int R, int shared_tokens) {
+  const int n_shared = shared_tokens / rows::TILE;
+  const int blocks = ((batch * R + 127) / 128) * rows::NKV;
+  const int want = 2 * device_cu_count() / blocks;
+  const int cap = n_shared / 2 > 0 ? n_shared / 2 : 1;
+  return want < 1 ? 1 : (want > cap ? cap : want);
+}
+
+// Counter region | partial O [2 G + B (S + 1) slots, n_kv, R, head_dim] | log-sum-exps, slots
+// 0 .. 2G-1 for the balanced ranges, 2G + b S + s for the prefix splits, 2G + B S + b for a
+// sequence whose suffix one range holds whole.
+static size_t ws_bytes_cascade(int grid, int R, int batch, int S) {
+  const size_t slots = size_t(2) * grid + size_t(batch) * (S + 1);
+  return kCounterBytes + slots * rows::NKV * R * (rows::HD + 2) * sizeof(float);
+}
+
+}  // namespace pkv
+
+extern "C" size_t pkv_cascade_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv,
+                                              int32_t head_dim, int32_t page_size, int32_t max_blocks,
+                                              int32_t shared_tokens) {
+  using namespace pkv;
+  if (batch <= 0 || s_q <= 0 || n_kv <= 0 || n_heads <= 0 || max_blocks <= 0 || page_size <= 0 || head_dim <= 0)
+    return 0;
+  const int R = s_q * (n_heads / n_kv);
+  if (!cascade_eligible(batch, head_dim, n_kv, R, page_size, max_blocks, shared_tokens))
+    return pkv_decode_workspace_bytes(batch, s_q, n_heads, n_kv, head_dim, page_size, max_blocks, 0);
+  return ws_bytes_cascade(lean_grid(0), R, batch, cascade_splits_for(batch, R, shared_tokens));
+}
+
+extern "C" int pkv_cascade_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, const void* k_new,
+                                int64_t kn_sb, int64_t kn_ss, int64_t kn_sh, const void* v_new, int64_t vn_sb,
+                                int64_t vn_ss, int64_t vn_sh, void* k_cache, void* v_cache, int64_t cache_page_stride,
+                                const int32_t* block_table, int64_t bt_stride, const int32_t* cache_seqlens, void* out,
+                                int64_t o_sb, int64_t o_ss, int64_t o_sh, void* workspace, size_t workspace_bytes,
+                                int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv, int32_t head_dim,
+                                int32_t page_size, int32_t num_pages, int32_t max_blocks, int32_t shared_tokens,
+                                int32_t causal, float softmax_scale, int32_t* status, void* stream) {
+  using namespace pkv;
+  clear_error();
+  const char* fn = "pkv_cascade_attn";
+  int rc = validate_attn(fn, q, q_sb, q_ss, q_sh, k_new, kn_sb, kn_ss, kn_sh, v_new, vn_sb, vn_ss, vn_sh, k_cache,
+                         v_cache, cache_page_stride, block_table, bt_stride, cache_seqlens, out, o_sb, o_ss, o_sh,
+                         batch, s_q, n_heads, n_kv, head_dim, page_size, num_pages, max_blocks, softmax_scale);
+  if (rc) return rc;
+  if (shared_tokens < 0) return fail(PKV_EINVAL, "%s: shared_tokens %d < 0", fn, shared_tokens);
+  const int R = s_q * (n_heads / n_kv);
+  if (R > 64) return fail(PKV_EINVAL, "%s: s_q * n_heads / n_kv = %d > 64; use pkv_prefill_attn", fn, R);
+  if (!cascade_eligible(batch, head_dim, n_kv, R, page_size, max_blocks, shared_tokens))
+    return pkv_decode_attn(q, q_sb, q_ss, q_sh, k_new, kn_sb, kn_ss, kn_sh, v_new, vn_sb, vn_ss, vn_sh, k_cache,
+                           v_cache, cache_page_stride, block_table, bt_stride, cache_seqlens, out, o_sb, o_ss, o_sh,
+                           workspace, workspace_bytes, batch, s_q, n_heads, n_kv, head_dim, page_size, num_pages,
+                           max_blocks, causal, softmax_scale, 0, 0, status, stream);
+  if (batch == 0) return PKV_OK;
+  const int grid = lean_grid(0);
+  const int S = cascade_splits_for(batch, R, shared_tokens);
+  const size_t need = ws_bytes_cascade(grid, R, batch, S);
+  if (need - kCounterBytes >= (size_t(1) << 31))
+    return fail(PKV_EINVAL, "%s: a %zu-byte workspace (partials must stay under 2 GiB)", fn, need);
+  if (!workspace || workspace_bytes < need)
+    return fail(PKV_ENOSPC, "%s: workspace %zu bytes < %zu needed", fn, workspace_bytes, need);
+  if (!aligned16(workspace)) return fail(PKV_EINVAL, "%s: workspace not 16-byte aligned", fn);
+
+  AttnParams p;
+  fill_params(p, q, q_sb, q_ss, q_sh, k_new, kn_sb, kn_ss, kn_sh, v_new, vn_sb, vn_ss, vn_sh, k_cache, v_cache,
+              cache_page_stride, block_table, bt_stride, cache_seqlens, out, o_sb, o_ss, o_sh, s_q, n_heads, n_kv,
+              page_size, num_pages, max_blocks, causal, softmax_scale, status);
+  p.batch = batch;
+  const size_t slots = size_t(2) * grid + size_t(batch) * (S + 1);
+  p.ws_cnt = static_cast<int32_t*>(workspace);
+  p.ws_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+  p.ws_ml = p.ws_o + slots * rows::NKV * R * rows::HD;
+  p.two_pass = 1;
+  p.lean_grid = grid;
+  p.k0 = shared_tokens;
+  p.cascade_splits = S;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  constexpr int NT = PKV_PREFILL_LDS_NT, W = PKV_PREFILL_LDS_W;
+  const dim3 pgrid((batch * R + 16 * NT * W - 1) / (16 * NT * W), rows::NKV, S);
+  prefill_lds_kernel<NT, W, PKV_PREFILL_LDS_NBUF, PKV_PREFILL_LDS_SUB, true><<<pgrid, 64 * W, 0, s>>>(p);
+  switch ((R + 15) / 16) {
+    case 1: decode_lean_kernel<1><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
+    case 2: decode_lean_kernel<2><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
+    case 3: decode_lean_kernel<3><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
+    default: decode_lean_kernel<4><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
+  }
+  combine_lean_kernel<<<dim3(rows::NKV, batch, (R + 15) / 16), 64 * (R < 16 ? R : 16), 0, s>>>(p, grid);
   return check_launch(fn);
 }
 

@@ -1,0 +1,109 @@
+"""GPU parity of cascade (shared-prefix) attention, pkv_cascade_attn through the C ABI: batches
+whose sequences list the same pages for a shared prefix, each with its own suffix and new rows,
+against the fp64 oracle (which knows nothing of the sharing) and against the ordinary decode path,
+plus the input checks (a sequence not sharing the prefix, or shorter than it, is flagged)."""
+import numpy as np
+import pytest
+import torch
+
+import prism_amd
+from oracle import paged_attention as pa
+from pkv_testutil import assert_attn_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _shared_case(gpu, *, suffix, shared_pages, page_size, s_q, n_heads=28, n_kv=4, hd=128, seed=0,
+                 break_row=None):
+    """Pool + block tables: every sequence's first `shared_pages` columns are the same pages;
+    sequence b holds shared_pages * P + suffix[b] keys before the append."""
+    g = torch.Generator().manual_seed(seed)
+    B = len(suffix)
+    shared = shared_pages * page_size
+    ctx = np.array([shared + s for s in suffix], dtype=np.int64)
+    own = [int(np.ceil((c + s_q) / page_size)) - shared_pages for c in ctx]
+    num_pages = shared_pages + sum(own) + 4
+    perm = torch.randperm(num_pages, generator=g).to(torch.int32)
+    width = shared_pages + max(own)
+    bt = torch.zeros(B, width, dtype=torch.int32)
+    off = shared_pages
+    for b in range(B):
+        bt[b, :shared_pages] = perm[:shared_pages]
+        bt[b, shared_pages:shared_pages + own[b]] = perm[off:off + own[b]]
+        off += own[b]
+    if break_row is not None:
+        bt[break_row, 0] = perm[-1]  # a page outside the shared set (still inside the pool)
+    kc = torch.randn(num_pages, page_size, n_kv, hd, generator=g).to(torch.bfloat16)
+    vc = torch.randn(num_pages, page_size, n_kv, hd, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, s_q, n_heads, hd, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, s_q, n_kv, hd, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, s_q, n_kv, hd, generator=g).to(torch.bfloat16)
+    sl = torch.tensor(ctx, dtype=torch.int32)
+    cpu = dict(q=q, k=k, v=v, k_cache=kc, v_cache=vc, block_table=bt, cache_seqlens=sl)
+    return cpu, {n: t.to(gpu) for n, t in cpu.items()}, shared
+
+
+CASES = [
+    # (suffix lengths, shared pages, page size, s_q)
+    ([(i * 97) % 300 for i in range(64)], 2, 256, 5),   # config-5 shape, smaller: R = 35
+    ([0, 31, 200], 3, 32, 1),                            # a suffix of zero keys; R = 7
+    ([(i * 53) % 170 for i in range(40)], 2, 64, 2),     # R = 14, suffixes at tile / page edges
+    ([5, 0, 700, 33, 64, 1, 250, 96], 1, 256, 8),       # R = 56: four row tiles per wave
+    ([3000, 17], 4, 256, 5),                             # one long suffix: many ranges per sequence
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"c{i}" for i in range(len(CASES))])
+def test_cascade_matches_oracle_and_plain_decode(gpu, case):
+    suffix, shared_pages, P, s_q = case
+    print(f"cascade case B={len(suffix)} shared={shared_pages}x{P} s_q={s_q}", flush=True)
+    cpu, dev, shared = _shared_case(gpu, suffix=suffix, shared_pages=shared_pages, page_size=P, s_q=s_q)
+    kc0, vc0 = dev["k_cache"].clone(), dev["v_cache"].clone()
+    out = torch.full_like(dev["q"], float("nan"))
+    prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], dev["k"], dev["v"],
+                                      cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"],
+                                      causal=True, shared_prefix_tokens=shared, out=out)
+    torch.cuda.synchronize()
+    ref, kb, vb = pa.flash_attn_with_kvcache_ref(cpu["q"], cpu["k_cache"], cpu["v_cache"], cpu["k"], cpu["v"],
+                                                 cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"],
+                                                 causal=True)
+    assert np.array_equal(pa.bf16_bits(dev["k_cache"]), kb), "K cache not bit-exact after append"
+    assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "V cache not bit-exact after append"
+    assert_attn_close(out, ref, f"cascade {case}")
+    # the ordinary path on the same inputs (a fresh copy of the caches) agrees to rounding
+    plain = prism_amd.flash_attn_with_kvcache(dev["q"], kc0, vc0, dev["k"], dev["v"],
+                                              cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"],
+                                              causal=True)
+    torch.cuda.synchronize()
+    diff = (plain.float() - out.float()).abs()
+    assert float(diff.max()) <= 1.6e-2, f"cascade vs plain decode: max diff {float(diff.max())}"
+    assert prism_amd.read_status(gpu) == 0
+
+
+def test_cascade_flags_a_sequence_outside_the_prefix(gpu):
+    cpu, dev, shared = _shared_case(gpu, suffix=[10, 20, 30], shared_pages=2, page_size=32, s_q=5, break_row=1)
+    prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], dev["k"], dev["v"],
+                                      cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"],
+                                      causal=True, shared_prefix_tokens=shared)
+    torch.cuda.synchronize()
+    assert prism_amd.read_status(gpu) & prism_amd._lib.PKV_STATUS_SHARED_PREFIX
+    # a sequence shorter than the declared prefix
+    cpu, dev, shared = _shared_case(gpu, suffix=[10, 20, 30], shared_pages=2, page_size=32, s_q=5)
+    prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], dev["k"], dev["v"],
+                                      cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"],
+                                      causal=True, shared_prefix_tokens=shared + 32)
+    torch.cuda.synchronize()
+    assert prism_amd.read_status(gpu) & prism_amd._lib.PKV_STATUS_SHARED_PREFIX
+
+
+def test_cascade_falls_back_off_page_boundaries(gpu):
+    # a prefix that is not a whole number of pages runs the ordinary decode path
+    cpu, dev, shared = _shared_case(gpu, suffix=[10, 300, 0], shared_pages=2, page_size=256, s_q=5)
+    out = prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], dev["k"], dev["v"],
+                                            cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"],
+                                            causal=True, shared_prefix_tokens=shared - 16)
+    torch.cuda.synchronize()
+    ref, _, _ = pa.flash_attn_with_kvcache_ref(cpu["q"], cpu["k_cache"], cpu["v_cache"], cpu["k"], cpu["v"],
+                                               cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"],
+                                               causal=True)
+    assert_attn_close(out, ref, "cascade fallback")
