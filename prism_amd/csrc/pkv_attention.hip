@@ -23,6 +23,8 @@
 // Every K/V byte of a (sequence, KV head) is fetched once per query-row tile.
 #include <math.h>
 
+#include <type_traits>
+
 #include "pkv_common.h"
 
 namespace pkv {
@@ -1781,7 +1783,36 @@ constexpr int ROW = HD * 2;            // one KV head's slice of a token row: 25
 constexpr int TILE = 32;
 constexpr int KV_BYTES = TILE * ROW;   // 8 KiB of K (or V) per tile
 constexpr int BUF = 2 * KV_BYTES;      // K | V
+// 16-byte chunk swizzle of V row r (LDS chunk c holds global chunk c ^ swz_v(r)).  A transpose
+// read of V^T operand n touches, in each half wave, token rows 8 q + 4 h + j (j < 4, q one of two
+// adjacent values) at global chunks 2 n and 2 n + 1: bits 1..3 of the swizzle take 8 distinct
+// values over those rows, so the 8 chunk pairs fall in 8 different bank ranges.
+__device__ __forceinline__ int swz_v(int r) { return ((r & 3) << 1) | (((r >> 3) & 1) << 3); }
 }  // namespace pf
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((const rows::lds_void*)p));
+}
+
+// LDS transpose reads (ds_read_b64_tr_b16) issued from inline assembly, and their wait.  The
+// compiler's builtin for this instruction makes it wait for every outstanding global-to-LDS copy
+// first (vmcnt(0)), which would drain the copy pipeline of the next tiles on every tile; as
+// assembly the read issues at once.  The compiler does not track these reads: the values must not
+// be touched before lds_tr_wait, which waits for every outstanding LDS access and hands the
+// registers on (its "+v" operands keep every use of them after the wait).
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_read_tr16_issue(uint32_t addr) {
+  u32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+
+__device__ __forceinline__ void lds_tr_wait(u32x2 (&a)[8], u32x2 (&b)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7]),
+                 "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]), "+v"(b[4]), "+v"(b[5]), "+v"(b[6]), "+v"(b[7]));
+}
 
 template <int OPS, int NBUF>
 __device__ __forceinline__ void pf_wait(int ahead) {
@@ -1800,10 +1831,21 @@ __device__ __forceinline__ void pf_wait(int ahead) {
 // MFMA chains), then the softmax of all tiles with one wave-uniform rescale test, then every PV
 // product.  The row max is taken on raw scores (the scale is positive) and the scale is folded
 // into the exponent's FMA.  P is rounded to bf16 once (prefill has no MFMA headroom to spare).
-template <int NT>
-__device__ __forceinline__ void compute_tile_prefill(const AttnParams& p, const KVTile<128>& tl, int T0,
-                                                     const bf16x8 (&qf)[NT][4], const int (&lim)[NT], int lim_min,
-                                                     float (&m_run)[NT], float (&l_run)[NT], f32x4 (&acc)[NT][8]) {
+// The update itself, on ready operands: kr the tile's K rows (QK^T A operands), vt[n] the V^T
+// A operands (lane (i, q): 8 keys 8 q .. 8 q + 7 of one head-dim element per operand; which
+// element lane i holds in operand n is the caller's layout, and the accumulator row of that lane
+// follows it).
+// l_run is either a per-lane partial row sum (float: this lane's keys, summed over the four lanes
+// of a row at the end) or the whole row sum kept by the matrix cores (f32x4: P times a ones
+// operand, every element the row's sum, of the same bf16 P the PV product uses), which takes the
+// 16 additions per tile off the vector ALU for NT extra products.
+template <int NT, typename LT, typename VIssue, typename VOps>
+__device__ __forceinline__ void compute_tile_prefill_ops(const AttnParams& p, const u32x4 (&kr)[2][4],
+                                                         VIssue&& v_issue, VOps&& v_ops, int T0,
+                                                         const bf16x8 (&qf)[NT][4],
+                                                         const int (&lim)[NT], int lim_min, float (&m_run)[NT],
+                                                         LT (&l_run)[NT], f32x4 (&acc)[NT][8]) {
+  constexpr bool kLByMfma = std::is_same<LT, f32x4>::value;
   constexpr int DPL = 8;
   const int lane = threadIdx.x & 63;
   const int lq = lane >> 4;
@@ -1815,19 +1857,10 @@ __device__ __forceinline__ void compute_tile_prefill(const AttnParams& p, const 
       s[nt][a] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
-        s[nt][a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, tl.kr[a][kk]), qf[nt][kk],
+        s[nt][a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[a][kk]), qf[nt][kk],
                                                            s[nt][a], 0, 0, 0);
     }
-  bf16x8 vt[DPL];
-#pragma unroll
-  for (int n = 0; n < DPL; ++n) {
-    const int w = n >> 1;
-    const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
-    u32x4 pk;
-#pragma unroll
-    for (int pp = 0; pp < 4; ++pp) pk[pp] = __builtin_amdgcn_perm(tl.vr[2 * pp + 1].w[w], tl.vr[2 * pp].w[w], sel);
-    vt[n] = __builtin_bit_cast(bf16x8, pk);
-  }
+  v_issue();
   if (T0 + 31 > lim_min) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
@@ -1837,19 +1870,22 @@ __device__ __forceinline__ void compute_tile_prefill(const AttnParams& p, const 
         for (int r = 0; r < 4; ++r)
           if (T0 + 8 * lq + 4 * a + r > lim[nt]) s[nt][a][r] = -INFINITY;
   }
-  float mx[NT];
+  // The rescale test runs on each lane's own 8 scores: scaling by the positive scale_log2 keeps
+  // the order, so some lane of a row passes it exactly when the row's maximum does.  Only then is
+  // the row maximum taken across the row's four lanes.
+  float lmax[NT];
   bool grow_any = false;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const float m = max3_raw(max3_raw(s[nt][0][0], s[nt][0][1], s[nt][0][2]),
-                             max3_raw(s[nt][0][3], s[nt][1][0], s[nt][1][1]), max_raw(s[nt][1][2], s[nt][1][3]));
-    mx[nt] = max_over_quads(m) * p.scale_log2;
-    grow_any |= mx[nt] > m_run[nt] + kRescaleSlack;
+    lmax[nt] = max3_raw(max3_raw(s[nt][0][0], s[nt][0][1], s[nt][0][2]),
+                        max3_raw(s[nt][0][3], s[nt][1][0], s[nt][1][1]), max_raw(s[nt][1][2], s[nt][1][3]));
+    grow_any |= lmax[nt] * p.scale_log2 > m_run[nt] + kRescaleSlack;
   }
   if (__any(grow_any)) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const float m_new = mx[nt] > m_run[nt] + kRescaleSlack ? mx[nt] : m_run[nt];
+      const float mx = max_over_quads(lmax[nt]) * p.scale_log2;
+      const float m_new = mx > m_run[nt] + kRescaleSlack ? mx : m_run[nt];
       const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[nt] - m_new);  // see compute_tile
       l_run[nt] *= alpha;
 #pragma unroll
@@ -1867,17 +1903,45 @@ __device__ __forceinline__ void compute_tile_prefill(const AttnParams& p, const 
     for (int e = 0; e < 8; e += 2) {
       const float p0 = fast_exp2(fmaf(s[nt][e >> 2][e & 3], p.scale_log2, neg_m));
       const float p1 = fast_exp2(fmaf(s[nt][e >> 2][(e & 3) + 1], p.scale_log2, neg_m));
-      psum += p0 + p1;
+      if constexpr (!kLByMfma) psum += p0 + p1;
       pk[e >> 1] = pack_bf16x2(p0, p1);
     }
-    l_run[nt] += psum;
+    if constexpr (!kLByMfma) l_run[nt] += psum;
     pb[nt] = __builtin_bit_cast(bf16x8, pk);
   }
+  if constexpr (kLByMfma) {
+    const u32x4 one2 = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0 pairs
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      l_run[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, one2), pb[nt], l_run[nt], 0, 0, 0);
+  }
+  bf16x8 vt[DPL];
+  v_ops(vt);
 #pragma unroll
   for (int n = 0; n < DPL; ++n)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
       acc[nt][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[n], pb[nt], acc[nt][n], 0, 0, 0);
+}
+
+// The same update on a tile read row-wise (KVTile): V^T operand n of lane (i, q) is head-dim
+// element 8 i + n, gathered from the V rows by byte permutes.
+template <int NT>
+__device__ __forceinline__ void compute_tile_prefill(const AttnParams& p, const KVTile<128>& tl, int T0,
+                                                     const bf16x8 (&qf)[NT][4], const int (&lim)[NT], int lim_min,
+                                                     float (&m_run)[NT], float (&l_run)[NT], f32x4 (&acc)[NT][8]) {
+  auto v_ops = [&](bf16x8 (&vt)[8]) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const int w = n >> 1;
+      const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
+      u32x4 pk;
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) pk[pp] = __builtin_amdgcn_perm(tl.vr[2 * pp + 1].w[w], tl.vr[2 * pp].w[w], sel);
+      vt[n] = __builtin_bit_cast(bf16x8, pk);
+    }
+  };
+  compute_tile_prefill_ops<NT>(p, tl.kr, [] {}, v_ops, T0, qf, lim, lim_min, m_run, l_run, acc);
 }
 
 // Input check of a cascade launch, by one wave: sequences b0..b1 must each hold at least k0 keys
@@ -1961,6 +2025,9 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
     load_q_batch_rows<HD, NT>(p, h, row0, p.k0 - 1, qf, lim);
   else
     load_q<HD, NT>(p, sv, L, row0, qf, lim);
+  // Q is in registers before any tile copy goes out: the tile loop's waits then never have to
+  // account for it (the copy pipeline's own waits are the explicit pf_wait ones)
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   int lim_min = 0x7fffffff;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) lim_min = min(lim_min, lim[nt] < 0 ? 0x7fffffff : lim[nt]);
@@ -1973,7 +2040,18 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
   const int row_elems = p.n_kv * HD;
   // Stage st holds tiles SUB*st .. SUB*st + SUB-1 (the last stage repeats its last real tile so
   // every stage issues the same number of copies).  Copy instruction i of a tile: K (i < 8) or V
-  // rows 4 (i % 8) .. +3, lane l -> row + l / 16, LDS chunk l % 16 <- global chunk (l % 16) ^ swz(row).
+  // rows 4 (i % 8) .. +3, lane l -> row + l / 16, LDS chunk l % 16 <- global chunk (l % 16) ^ swizzle
+  // (swz for K rows, swz_v for V rows).
+  // The copies are buffer loads: a tile's K and V rows of this head are one buffer each (base and
+  // range in scalar registers), and each lane's byte offset inside it is the same for every tile.
+  uint32_t voff[16 / W];
+#pragma unroll
+  for (int k = 0; k < 16 / W; ++k) {
+    const int i = wave + k * W;
+    const int r = 4 * (i & 7) + (lane >> 4);
+    voff[k] = uint32_t(r * row_elems + ((lane & 15) ^ (i < 8 ? rows::swz(r) : pf::swz_v(r))) * 8) * 2u;
+  }
+  const int tile_bytes = pf::TILE * row_elems * 2;
   auto issue = [&](int st) {
     char* stage = lds + (st % NBUF) * SUB * pf::BUF;
 #pragma unroll
@@ -1988,22 +2066,37 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
 #pragma unroll
       for (int k = 0; k < 16 / W; ++k) {
         const int i = wave + k * W;
-        const int r = 4 * (i & 7) + (lane >> 4);
-        const int gc = (lane & 15) ^ rows::swz(r);
-        const uint16_t* src = (i < 8 ? p.k_cache : p.v_cache) + off + int64_t(r) * row_elems + gc * 8;
-        __builtin_amdgcn_global_load_lds(src, (rows::lds_void*)(buf + (i >= 8 ? pf::KV_BYTES : 0) + (i & 7) * 1024),
-                                         16, 0, 0);
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            uniform_ptr((i < 8 ? p.k_cache : p.v_cache) + off), 0, tile_bytes, 0x00020000);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs,
+                                                 (rows::lds_void*)(buf + (i >= 8 ? pf::KV_BYTES : 0) + (i & 7) * 1024),
+                                                 16, int(voff[k]), 0, 0, 0);
       }
     }
   };
   for (int st = 0; st < NBUF && st < n_stages; ++st) issue(st);
+  // V^T operands come from LDS transpose reads (ds_read_b64_tr_b16): in each 16-lane group, lane
+  // 4 j + c names 4 consecutive elements of row j of a 4 x 16 block of 16-bit values and receives
+  // column (its index in the group) of that block.  Operand n of lane (li, lq) is head-dim element
+  // 16 n + li over keys 8 lq .. 8 lq + 7: two reads, of token rows 8 lq + j and 8 lq + 4 + j (the
+  // same swizzle, 4 rows further), each lane naming elements 16 n + 4 c .. + 3.  vtr[n] is that
+  // lane's byte offset inside a tile's V rows, the same for every tile.
+  uint32_t vtr[8];
+  {
+    const int t = 8 * lq + (li >> 2);
+    const int c = li & 3;
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+      vtr[n] = uint32_t(t * pf::ROW + (((2 * n + (c >> 1)) ^ pf::swz_v(t)) << 4) + 8 * (c & 1));
+  }
 
-  float m_run[NT], l_run[NT];
+  float m_run[NT];
+  f32x4 l_run[NT];  // row sums kept by the matrix cores (every element the row's sum)
   f32x4 acc[NT][DPL];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     m_run[nt] = -INFINITY;
-    l_run[nt] = 0.f;
+    l_run[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int n = 0; n < DPL; ++n) acc[nt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -2016,31 +2109,46 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
       if (t >= n_tiles) break;
       const int T0 = (t_first + t) * pf::TILE;
       const char* buf = lds + ((st % NBUF) * SUB + u) * pf::BUF;
-      KVTile<HD> tl;
+      u32x4 kr[2][4];
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         const int r = 8 * (li >> 2) + 4 * a + (li & 3);
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk)
-          tl.kr[a][kk] = *reinterpret_cast<const u32x4*>(buf + r * pf::ROW + (((4 * kk + lq) ^ rows::swz(r)) << 4));
+          kr[a][kk] = *reinterpret_cast<const u32x4*>(buf + r * pf::ROW + (((4 * kk + lq) ^ rows::swz(r)) << 4));
       }
+      // the V^T reads go out once the QK products are issued (so the compiler's waits for the K
+      // reads, which do not count these, stay exact) and are waited for just before the PV
+      // products (lds_tr_wait): their latency hides behind the QK products and the softmax
+      const uint32_t vrows = lds_addr(buf + pf::KV_BYTES);
+      u32x2 vlo[8], vhi[8];
+      auto v_issue = [&] {
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int r = 8 * lq + e;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(buf + pf::KV_BYTES + r * pf::ROW + ((li ^ rows::swz(r)) << 4));
-#pragma unroll
-        for (int w = 0; w < 4; ++w) tl.vr[e].w[w] = v[w];
-      }
-      if (T0 + pf::TILE > L) {
-        // rows past the sequence: P = 0 must not meet a stale NaN
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const bool keep = T0 + 8 * lq + e < L;
-#pragma unroll
-          for (int w = 0; w < 4; ++w) tl.vr[e].w[w] = keep ? tl.vr[e].w[w] : 0u;
+        for (int n = 0; n < 8; ++n) {
+          vlo[n] = lds_read_tr16_issue<0>(vrows + vtr[n]);
+          vhi[n] = lds_read_tr16_issue<4 * pf::ROW>(vrows + vtr[n]);
         }
-      }
-      if (row0 < R_all) compute_tile_prefill<NT>(p, tl, T0, qf, lim, lim_min, m_run, l_run, acc);
+      };
+      auto v_ops = [&](bf16x8 (&vt)[8]) {
+        lds_tr_wait(vlo, vhi);
+        u32x4 vw[8];
+#pragma unroll
+        for (int n = 0; n < 8; ++n) vw[n] = u32x4{vlo[n][0], vlo[n][1], vhi[n][0], vhi[n][1]};
+        if (T0 + pf::TILE > L) {
+          // keys past the sequence: P = 0 must not meet a stale NaN (word w holds keys 2 w, 2 w + 1)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const int k = T0 + 8 * lq + 2 * w;
+            const uint32_t keep = (k < L ? 0x0000FFFFu : 0u) | (k + 1 < L ? 0xFFFF0000u : 0u);
+#pragma unroll
+            for (int n = 0; n < 8; ++n) vw[n][w] &= keep;
+          }
+        }
+#pragma unroll
+        for (int n = 0; n < 8; ++n) vt[n] = __builtin_bit_cast(bf16x8, vw[n]);
+      };
+      if (row0 < R_all) compute_tile_prefill_ops<NT>(p, kr, v_issue, v_ops, T0, qf, lim, lim_min, m_run, l_run, acc);
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the stage are done
     raw_barrier();                       // the stage's buffer is free
@@ -2055,20 +2163,22 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int ra = row0 + li + 16 * nt;
-      const float lsum = sum_over_quads(l_run[nt]);
+      const float lsum = l_run[nt][0];
       if (ra < R_all) {
         const int br = ra / p.R;
         const int rr = ra - br * p.R;
         const int slot = 2 * p.lean_grid + br * p.cascade_splits + int(blockIdx.z);
         const uint32_t row = uint32_t((slot * rows::NKV + h) * p.R + rr);
         const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-        u32x4 ov[4];
+        // accumulator n of lane (li, lq) holds head-dim elements 16 n + 4 lq .. + 3
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int k = 0; k < 4; ++k) ov[r][k] = pack_f16x2(acc[nt][2 * k][r] * inv, acc[nt][2 * k + 1][r] * inv);
+        for (int n = 0; n < DPL; ++n) {
+          const u32x2 ov = {pack_f16x2(acc[nt][n][0] * inv, acc[nt][n][1] * inv),
+                            pack_f16x2(acc[nt][n][2] * inv, acc[nt][n][3] * inv)};
+          __builtin_amdgcn_raw_buffer_store_b64(ov, rs, int((row * HD + 16 * n + 4 * lq) * 2u), 0, 0);
+        }
         const float lse = lsum > 0.f ? m_run[nt] + __builtin_amdgcn_logf(lsum) : -INFINITY;
-        ws_store_partial<0>(rs, (row * HD + 4 * DPL * lq) * 2u, ov, lq == 0, lse0 + row * 4u, lse);
+        if (lq == 0) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, lse), rs, int(lse0 + row * 4u), 0, 0);
       }
     }
     return;
@@ -2077,18 +2187,17 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int row = row0 + li + 16 * nt;
-    const float lsum = sum_over_quads(l_run[nt]);
+    const float lsum = l_run[nt][0];
     if (row < p.R) {
       const int j = row / p.g;
       const int hq = row - j * p.g;
       const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-      uint16_t* dst = p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + 4 * DPL * lq;
+      uint16_t* dst = p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + 4 * lq;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        u32x4 ov;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[nt][2 * k][r] * inv, acc[nt][2 * k + 1][r] * inv);
-        st16(dst + DPL * r, ov);
+      for (int n = 0; n < DPL; ++n) {
+        const u32x2 ov = {pack_bf16x2(acc[nt][n][0] * inv, acc[nt][n][1] * inv),
+                          pack_bf16x2(acc[nt][n][2] * inv, acc[nt][n][3] * inv)};
+        *reinterpret_cast<u32x2*>(dst + 16 * n) = ov;
       }
     }
   }
