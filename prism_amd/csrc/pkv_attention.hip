@@ -2074,7 +2074,12 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
       }
     }
   };
-  for (int st = 0; st < NBUF && st < n_stages; ++st) issue(st);
+  // NBUF == 2: stage st + 2 is issued into st's buffer once every wave has read it (a second
+  // barrier per tile).  NBUF >= 3: stage st + NBUF - 1 is issued into the buffer of stage st - 1
+  // right after the tile's first barrier, which every wave passes only after it has consumed
+  // stage st - 1: one barrier per tile, and NBUF - 1 stages in flight during the compute.
+  constexpr bool kOneBarrier = NBUF >= 3;
+  for (int st = 0; st < (kOneBarrier ? NBUF - 1 : NBUF) && st < n_stages; ++st) issue(st);
   // V^T operands come from LDS transpose reads (ds_read_b64_tr_b16): in each 16-lane group, lane
   // 4 j + c names 4 consecutive elements of row j of a 4 x 16 block of 16-bit values and receives
   // column (its index in the group) of that block.  Operand n of lane (li, lq) is head-dim element
@@ -2101,8 +2106,14 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
     for (int n = 0; n < DPL; ++n) acc[nt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   for (int st = 0; st < n_stages; ++st) {
-    pf_wait<OPS, NBUF>(min(NBUF - 1, n_stages - 1 - st));
-    raw_barrier();
+    if constexpr (kOneBarrier) {
+      pf_wait<OPS, NBUF>(min(NBUF - 2, n_stages - 1 - st));
+      raw_barrier();
+      if (st + NBUF - 1 < n_stages) issue(st + NBUF - 1);
+    } else {
+      pf_wait<OPS, NBUF>(min(NBUF - 1, n_stages - 1 - st));
+      raw_barrier();
+    }
 #pragma unroll
     for (int u = 0; u < SUB; ++u) {
       const int t = st * SUB + u;
@@ -2150,9 +2161,11 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
       };
       if (row0 < R_all) compute_tile_prefill_ops<NT>(p, kr, v_issue, v_ops, T0, qf, lim, lim_min, m_run, l_run, acc);
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the stage are done
-    raw_barrier();                       // the stage's buffer is free
-    if (st + NBUF < n_stages) issue(st + NBUF);
+    if constexpr (!kOneBarrier) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the stage are done
+      raw_barrier();                       // the stage's buffer is free
+      if (st + NBUF < n_stages) issue(st + NBUF);
+    }
   }
   if (row0 >= R_all) return;
   if constexpr (CASCADE) {
@@ -2363,7 +2376,7 @@ constexpr int kPrefillW = 4;
 #define PKV_PREFILL_LDS_W 4
 #endif
 #ifndef PKV_PREFILL_LDS_NBUF
-#define PKV_PREFILL_LDS_NBUF 2
+#define PKV_PREFILL_LDS_NBUF 4  // 64 KiB of LDS per workgroup, one barrier per tile
 #endif
 
 #ifndef PKV_PREFILL_LDS_SUB
