@@ -177,6 +177,7 @@ PREFILL_CASES = [
     (3, [0, 33, 290], 32, 4, 28, 128, 37),
     (2, [5, 1000], 256, 2, 14, 64, 100),
     (1, [0], 256, 4, 4, 128, 300),
+    (3, [2100, 4000, 1], 256, 8, 40, 128, 64),  # 14B shape, long tile loops through the 4-stage pipeline
 ]
 
 
