@@ -1772,8 +1772,9 @@ __global__ __launch_bounds__(64 * W) void prefill_kernel(const AttnParams p) {
 // KV head, sequence).  The W waves of a workgroup own 16*NT consecutive query rows each (row =
 // j * g + head-in-group, so a block spans a few query positions of every head of the group) and
 // share each 32-token K / V tile of their KV head: the workgroup copies a tile into LDS once
-// (16 global_load_lds_dwordx4 of 1 KiB, 16 / W per wave), NBUF tiles in flight, and every wave
-// reads its MFMA operands from there (chunks XOR-swizzled by swz(row) as in the decode kernel).
+// (16 buffer loads of 1 KiB straight into LDS, 16 / W per wave) into one of NBUF stage buffers,
+// and every wave reads its MFMA operands from there (16-byte chunks XOR-swizzled per row: K rows
+// by swz as in the decode kernel, V rows by swz_v for the transpose reads).
 // The block walks keys up to its last row's last visible key; rows that see fewer keys are masked
 // inside the tiles that cross their limit.  No split-K: every wave writes its own rows.
 // ---------------------------------------------------------------------------------------------
