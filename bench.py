@@ -70,8 +70,14 @@ def profiled_traffic(args, w):
     return None, None
 
 
-def cpu_baseline(w, n_layers: int, metric_unit: str) -> dict:
-    """The oracle's torch-CPU path (index_select page gather + fp32 SDPA) on n_layers of the workload."""
+def cpu_baseline(w, n_layers: int, metric_unit: str, gpu_outs=None) -> tuple[dict, dict | None]:
+    """The oracle's torch-CPU path (index_select page gather + fp32 SDPA) on n_layers of the workload,
+    timed, and its first run's results used as the parity check of the GPU run that preceded it.
+
+    gpu_outs: {name: per-layer GPU outputs} of the timed run(s).  The GPU already appended this call's
+    rows, and the CPU path appends the same rows again (the call is idempotent), so the append was
+    bit-exact iff the CPU append leaves the gathered pages unchanged; the GPU outputs are compared with
+    the fp32 CPU outputs at the north_star tolerance (max-abs <= 1e-2, mean-abs <= 1e-3)."""
     import torch
 
     from oracle import paged_attention as pa
@@ -85,7 +91,7 @@ def cpu_baseline(w, n_layers: int, metric_unit: str) -> dict:
     used = sorted({int(p) for b in range(w.batch) for p in bt[b, : -(-(int(sl[b]) + w.s_q) // kv.page_size)]})
     remap = torch.full((kv.max_pages,), 0, dtype=torch.int64)
     remap[torch.tensor(used)] = torch.arange(len(used))
-    bt_host = remap[bt.long()].to(torch.int32)
+    bt_host = remap[bt.long().clamp(min=0)].to(torch.int32)
     idx = torch.tensor(used, device=kv.k_pool.device)
     layers = []
     for l in range(n_layers):
@@ -93,8 +99,30 @@ def cpu_baseline(w, n_layers: int, metric_unit: str) -> dict:
                        w.q[l].cpu(), w.k[l].cpu(), w.v[l].cpu()))
 
     def run():
-        for kc, vc, q, k, v in layers:
-            pa.flash_attn_cpu(q, kc, vc, k, v, cache_seqlens=sl, block_table=bt_host, causal=True)
+        return [pa.flash_attn_cpu(q, kc, vc, k, v, cache_seqlens=sl, block_table=bt_host, causal=True)
+                for kc, vc, q, k, v in layers]
+
+    parity = None
+    if gpu_outs:
+        pre = [(kc.clone(), vc.clone()) for kc, vc, _, _, _ in layers]
+        ref = run()
+        exact = all(torch.equal(kc, a) and torch.equal(vc, b) for (kc, vc, _, _, _), (a, b) in zip(layers, pre))
+        del pre
+        parity = {"reference": "oracle.flash_attn_cpu: index_select page gather + fp32 SDPA (enable_gqa), "
+                               "bottom-right causal", "layers": list(range(n_layers)),
+                  "append_bit_exact": bool(exact), "tol_max_abs": 1e-2, "tol_mean_abs": 1e-3}
+        for name, outs in gpu_outs.items():
+            errs = [(outs[l].float().cpu() - ref[l]).abs() for l in range(n_layers)]
+            finite = all(bool(torch.isfinite(outs[l].float()).all()) for l in range(n_layers))
+            mx = max(float(e.max()) for e in errs)
+            mean = sum(float(e.sum()) for e in errs) / sum(e.numel() for e in errs)
+            parity[name] = {"max_abs": float(f"{mx:.3e}"), "mean_abs": float(f"{mean:.3e}"),
+                            "pass": finite and mx <= 1e-2 and mean <= 1e-3}
+        parity["pass"] = exact and all(v["pass"] for k, v in parity.items() if isinstance(v, dict))
+        print(f"[bench] parity vs CPU reference on {n_layers} layers: "
+              + ", ".join(f"{k} max-abs {v['max_abs']} mean-abs {v['mean_abs']}" for k, v in parity.items()
+                          if isinstance(v, dict))
+              + f", append bit-exact {exact}", file=sys.stderr, flush=True)
 
     reps = 5 if w.s_q == 1 else 2
     warm = min(3, reps)
@@ -122,7 +150,7 @@ def cpu_baseline(w, n_layers: int, metric_unit: str) -> dict:
         "us_per_step": round(per_layer * w.layers * 1e6, 1),
         "sample": f"{n_layers} of {w.layers} layers, all {w.batch} sequences, referenced pages only; "
                   f"{warm} warm-ups, median of {reps}; torch {torch.__version__} CPU, {model}",
-    }
+    }, parity
 
 
 def time_graph(fn, args, dev) -> float:
@@ -185,9 +213,16 @@ def config5_page_ops(prism_amd, w, dev) -> dict:
         dst = [kv.seq_pages[s][bidx] for s in w.seq_ids[1:]]
         src = [first] * len(dst)   # the same copy shape: fill slots of one page into every other child
         ms = time_eager(lambda: prism_amd.copy_pages(kv, kv, src, dst, [fill] * len(dst)), 20)
-        nbytes = 2 * len(dst) * fill * kv.num_kv_heads * kv.head_dim * 2 * 2 * L
+        slot_bytes = kv.num_kv_heads * kv.head_dim * 2
+        # HBM must move the source slots once and write every copy: (pages + 1) x fill slots per
+        # tensor; the kernel issues a read per copy, but 62 of the 63 reads of the one source page
+        # are cache hits, so they are not counted
+        nbytes = (len(dst) + 1) * fill * slot_bytes * 2 * L
+        issued = 2 * len(dst) * fill * slot_bytes * 2 * L
         out["copy_on_write"] = {"pages": len(dst), "fill_slots": fill, "us": round(ms * 1e3, 2), "bytes": nbytes,
-                                "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+                                "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                "pct_of_peak_hbm": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                                "bytes_issued": issued}
     live = kv.live_pages()
     fresh = prism_amd.FlashAttnKVCache(L, kv.num_kv_heads, kv.head_dim, len(live), kv.page_size, str(dev))
     ms = time_eager(lambda: prism_amd.copy_pages(kv, fresh, live, list(range(len(live))), None), 5)
@@ -599,7 +634,8 @@ def main() -> int:
     else:
         cfg["workload"] = ("config5: Qwen2.5-7B shared 2048-token prefix (ref-counted, copy-on-write boundary "
                            "page) + speculative verify of 5 draft tokens, 28 layers, b=64, suffix ~U{0..1024}")
-        cfg.update({k: v for k, v in w.meta.items() if k != "shape"})
+        cfg.update({k: v for k, v in w.meta.items() if k not in ("shape", "root_pages")})
+        outs_cascade = [torch.empty_like(q) for q in w.q]
         # cascade attention over the pages every child shares (the full pages of the prefix; the
         # boundary page was copied into each child): the prefix read once per layer for the batch
         shared_tokens = (w.meta["shared_prefix"] // kv.page_size) * kv.page_size
@@ -608,7 +644,8 @@ def main() -> int:
             for l in range(L):
                 prism_amd.flash_attn_with_kvcache(w.q[l], kv.k_caches[l], kv.v_caches[l], k=w.k[l], v=w.v[l],
                                                   cache_seqlens=w.cache_seqlens, block_table=w.block_table,
-                                                  causal=True, out=outs[l], shared_prefix_tokens=shared_tokens)
+                                                  causal=True, out=outs_cascade[l],
+                                                  shared_prefix_tokens=shared_tokens)
 
         cascade_ms = time_graph(cascade_step, args, dev)
         c_status = prism_amd.read_status(dev)
@@ -668,8 +705,14 @@ def main() -> int:
     if not args.no_cpu_baseline:
         n_cpu = min(args.cpu_layers if args.workload == "config3" else 1, L)
         print(f"[bench] cpu baseline on {n_cpu} layers", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(w, n_cpu, unit)
+        gpu_outs = {"out": outs}
+        if args.workload == "config5":
+            gpu_outs = {"verify": outs, "cascade": outs_cascade}
+        result["cpu_baseline"], result["parity"] = cpu_baseline(w, n_cpu, unit, gpu_outs)
     print(json.dumps(result), flush=True)
+    if result.get("parity") is not None and not result["parity"]["pass"]:
+        print("[bench] PARITY FAILED: the GPU results differ from the CPU reference", file=sys.stderr, flush=True)
+        return 3
     return 0
 
 

@@ -52,7 +52,11 @@ extern "C" {
 #define PKV_STATUS_BAD_PAGE 1
 #define PKV_STATUS_BAD_POSITION 2  /* a rotary position outside the cos/sin table (clamped) */
 #define PKV_STATUS_SHARED_PREFIX 4 /* pkv_cascade_attn: a sequence shorter than the shared prefix
-                                      or not listing its pages */
+                                      or not listing its pages, or (no append, causal) a query row
+                                      that may not see the whole prefix */
+#define PKV_STATUS_PARTIAL_RANGE 8 /* a balanced-kernel split-K partial (fp16 O / l) would exceed
+                                      fp16's range: |V| >= 65520 somewhere; that output is inf.
+                                      PKV_DECODE_HEADS keeps fp32 partials */
 
 /* pkv_decode_attn flags (0 = the library's choice of kernel and merge) */
 #define PKV_DECODE_TWO_PASS 1    /* merge split-K partials in a second launch */
@@ -85,7 +89,7 @@ int pkv_append(const void* k_new, int64_t kn_sb, int64_t kn_ss, int64_t kn_sh,
  * Bytes of workspace pkv_decode_attn needs for these sizes (split-K partial outputs and
  * log-sum-exp terms).  split_tokens = 0 asks for the library's own choice, exactly as
  * pkv_decode_attn would make it with flags = 0 (a PKV_DECODE_GRID(n) above the device's CU count
- * needs 65536 + 2 n * 4 * R * 130 * 4 bytes, R = s_q * n_heads / n_kv).
+ * needs 65536 + 2 n * 4 * R * 260 bytes, R = s_q * n_heads / n_kv).
  */
 size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv,
                                   int32_t head_dim, int32_t page_size, int32_t max_blocks,
@@ -111,8 +115,9 @@ size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, i
  * Otherwise a per-(sequence, KV head, split) kernel reduces split_tokens keys (a multiple of 32;
  * 0 = 512) per workgroup and merges the splits inside the launch (PKV_DECODE_TWO_PASS: in a
  * second launch).  Results agree up to rounding (fp32 order, fp16 split-K partials).
- * The balanced kernel keeps each split's normalised output in fp16, so it needs |V| < 65504
- * (bf16 V beyond that overflows the partial to inf); PKV_DECODE_HEADS keeps fp32 partials.
+ * The balanced kernel keeps each split's normalised output in fp16, so it needs |V| < 65520
+ * (bf16 V beyond that overflows the partial to inf and sets PKV_STATUS_PARTIAL_RANGE);
+ * PKV_DECODE_HEADS keeps fp32 partials.
  * workspace must hold pkv_decode_workspace_bytes() bytes and be
  * zero-filled before its first use; every call leaves it in that state again (its first 64 KiB
  * hold per-(sequence, KV head) arrival counters, so batch * n_kv <= 16384 when a sequence can

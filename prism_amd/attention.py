@@ -16,8 +16,10 @@ argument meaning:
 * returns a new bf16 ``out`` [B, s_q, n_heads, head_dim]; errors raise ``RuntimeError``.
 
 Calls are asynchronous on the caller's current stream, allocate only ``out`` (and a cached,
-grow-only split-K workspace per device), and can be captured in a HIP graph once the workspace
-has been sized by an eager call.
+grow-only split-K workspace per device and stream), and can be captured in a HIP graph once an
+eager call on the device has sized the workspace (on any stream: a capture stream without one of
+its own shares the largest, as Prism's warm-up on its current stream then capture on a new stream
+needs).
 """
 from __future__ import annotations
 
@@ -31,6 +33,7 @@ from . import _lib
 _BF16 = torch.bfloat16
 _ws_lock = threading.Lock()
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
+_retired: list[torch.Tensor] = []   # outgrown workspaces, kept alive for graphs that captured them
 _status: dict[int, torch.Tensor] = {}
 
 
@@ -65,20 +68,36 @@ def read_status(device: torch.device | str = "cuda", clear: bool = True) -> int:
 
 
 def _workspace(device: torch.device, nbytes: int, stream: int) -> torch.Tensor | None:
-    """Split-K workspace per (device, stream), grow-only.  Allocated zero-filled: its counter
-    region must start at zero, and every call leaves it zero again."""
+    """Split-K workspace per (device, stream), grow-only, allocated zero-filled: its counter
+    region must start at zero, and every call leaves it zero again.
+
+    Under HIP graph capture nothing may be allocated.  Prism warms up on its current stream and
+    then captures on a new one (engine/executor.py:186-197, :288-303), so a capture stream with
+    no workspace of its own takes the largest one an eager call on this device sized; the graph's
+    replays and the eager calls then share it, which is safe because Prism issues both from one
+    thread in order.  A workspace that grows is retired, never freed: a captured graph may still
+    hold its address."""
     if nbytes == 0:
         return None
     idx = device.index if device.index is not None else torch.cuda.current_device()
     key = (idx, stream)
     with _ws_lock:
         ws = _workspaces.get(key)
-        if ws is None or ws.numel() < nbytes:
-            if torch.cuda.is_current_stream_capturing():
+        if ws is not None and ws.numel() >= nbytes:
+            return ws
+        if torch.cuda.is_current_stream_capturing():
+            sized = [t for (d, _), t in _workspaces.items() if d == idx and t.numel() >= nbytes]
+            if not sized:
                 raise RuntimeError(
-                    "split-K workspace must be sized by an eager call before HIP graph capture")
+                    f"split-K workspace of {nbytes} bytes must be sized by an eager call on this device "
+                    "before HIP graph capture")
+            ws = max(sized, key=lambda t: t.numel())
+        else:
             ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-            _workspaces[key] = ws
+        old = _workspaces.get(key)
+        if old is not None:
+            _retired.append(old)
+        _workspaces[key] = ws
         return ws
 
 

@@ -1255,6 +1255,11 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));  // RNE
 }
+// A finite value fp16 cannot hold: under round-to-nearest-even everything from 65520 up becomes
+// inf (bf16 V rows beyond that magnitude; flagged as PKV_STATUS_PARTIAL_RANGE).
+__device__ __forceinline__ bool f16_overflows(float lo, float hi) {
+  return fmaxf(fabsf(lo), fabsf(hi)) >= 65520.f;
+}
 __device__ __forceinline__ void unpack_f16x8(const u32x4 v, float (&f)[8]) {
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
@@ -1542,6 +1547,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
         pub_last = d.b;
       const uint32_t lse0 = uint32_t(p.ws_ml - p.ws_o) * 4u;
       const __amdgpu_buffer_rsrc_t rs = ws_rsrc(p);
+      bool ovf = false;
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int rr = li + 16 * nt;
@@ -1552,7 +1558,11 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
 #pragma unroll
           for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int k = 0; k < 4; ++k) ov[r][k] = pack_f16x2(acc[nt][2 * k][r] * inv, acc[nt][2 * k + 1][r] * inv);
+            for (int k = 0; k < 4; ++k) {
+              const float lo = acc[nt][2 * k][r] * inv, hi = acc[nt][2 * k + 1][r] * inv;
+              ovf |= f16_overflows(lo, hi);
+              ov[r][k] = pack_f16x2(lo, hi);
+            }
           const float lse = lsum[nt] > 0.f ? m_run[nt] + __builtin_amdgcn_logf(lsum[nt]) : -INFINITY;
           const uint32_t o_off = (row * HD + 4 * DPL * lq) * 2u;
           if (p.two_pass)
@@ -1561,6 +1571,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
             ws_store_partial<kCoherent>(rs, o_off, ov, lq == 0, lse0 + row * 4u, lse);
         }
       }
+      if (__any(ovf) && lane == 0) flag_status(p.status, PKV_STATUS_PARTIAL_RANGE);
     }
   }
   if (p.two_pass || (pub_first < 0 && pub_last < 0)) return;
@@ -1945,17 +1956,20 @@ __device__ __forceinline__ void compute_tile_prefill(const AttnParams& p, const 
   compute_tile_prefill_ops<NT>(p, tl.kr, [] {}, v_ops, T0, qf, lim, lim_min, m_run, l_run, acc);
 }
 
-// Input check of a cascade launch, by one wave: sequences b0..b1 must each hold at least k0 keys
-// before the append and list sequence 0's first k0 / P pages (the prefix pass reads only those).
-// A violation flags PKV_STATUS_SHARED_PREFIX; the output of such a sequence is then meaningless,
-// but every access stays inside the pool.
+// Input check of a cascade launch, by one wave: sequences b0..b1 must list sequence 0's first
+// k0 / P pages (the prefix pass reads only those), and every query row must see all k0 prefix
+// keys, which the prefix pass gives it: at least k0 keys before an append; without an append,
+// causal row 0 of s_q sees keys [0, c - s_q], so c >= k0 + s_q - 1.  A violation flags
+// PKV_STATUS_SHARED_PREFIX; the output of such a sequence is then meaningless, but every access
+// stays inside the pool.
 __device__ __forceinline__ void cascade_check_sharing(const AttnParams& p, int b0, int b1) {
   if (threadIdx.x >= 64) return;
   const int lane = threadIdx.x & 63;
   const int np = p.k0 >> p.log2_page;
+  const int need = p.k0 + (p.has_new || !p.causal ? 0 : p.s_q - 1);
   bool bad = false;
   for (int b = b0; b <= b1 && b < p.batch; ++b) {
-    bad |= p.seqlens[b] < p.k0;
+    bad |= p.seqlens[b] < need;
     for (int c0 = 0; c0 < np; c0 += 64) {
       const int c = c0 + lane;
       if (c < np) bad |= p.block_table[int64_t(b) * p.bt_stride + c] != p.block_table[c];
@@ -2174,6 +2188,7 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
     // writes its partials
     const uint32_t lse0 = uint32_t(p.ws_ml - p.ws_o) * 4u;
     const __amdgpu_buffer_rsrc_t rs = ws_rsrc(p);
+    bool ovf = false;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int ra = row0 + li + 16 * nt;
@@ -2187,14 +2202,16 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
         // accumulator n of lane (li, lq) holds head-dim elements 16 n + 4 lq .. + 3
 #pragma unroll
         for (int n = 0; n < DPL; ++n) {
-          const u32x2 ov = {pack_f16x2(acc[nt][n][0] * inv, acc[nt][n][1] * inv),
-                            pack_f16x2(acc[nt][n][2] * inv, acc[nt][n][3] * inv)};
+          const f32x4 o = acc[nt][n] * inv;
+          ovf = ovf || f16_overflows(o[0], o[1]) || f16_overflows(o[2], o[3]);
+          const u32x2 ov = {pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
           __builtin_amdgcn_raw_buffer_store_b64(ov, rs, int((row * HD + 16 * n + 4 * lq) * 2u), 0, 0);
         }
         const float lse = lsum > 0.f ? m_run[nt] + __builtin_amdgcn_logf(lsum) : -INFINITY;
         if (lq == 0) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, lse), rs, int(lse0 + row * 4u), 0, 0);
       }
     }
+    if (__any(ovf) && lane == 0) flag_status(p.status, PKV_STATUS_PARTIAL_RANGE);
     return;
   }
 
@@ -2274,9 +2291,15 @@ static int lean_grid(int32_t flags) {
   return g > 0 ? g : device_cu_count();
 }
 
-// Same counter region | partial O [2 grid, n_kv, R, head_dim] | (m, l) [2 grid, n_kv, R, 2].
+// Same counter region | partial O / l [2 grid, n_kv, R, head_dim] fp16 | log-sum-exp
+// [2 grid, n_kv, R] fp32.
+constexpr size_t kLeanRowBytes = rows::HD * 2 + sizeof(float);
 static size_t ws_bytes_lean(int grid, int R) {
-  return kCounterBytes + size_t(2) * grid * rows::NKV * R * (rows::HD + 2) * sizeof(float);
+  return kCounterBytes + size_t(2) * grid * rows::NKV * R * kLeanRowBytes;
+}
+// First log-sum-exp float after `slots` fp16 partial blocks of n_kv x R rows.
+static float* lean_lse_base(float* ws_o, size_t slots, int R) {
+  return ws_o + slots * rows::NKV * R * rows::HD / 2;
 }
 
 static int validate_attn(const char* fn, const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, const void* k_new,
@@ -2418,18 +2441,18 @@ extern "C" size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t
   return need;
 }
 
-extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, const void* k_new,
-                               int64_t kn_sb, int64_t kn_ss, int64_t kn_sh, const void* v_new, int64_t vn_sb,
-                               int64_t vn_ss, int64_t vn_sh, void* k_cache, void* v_cache, int64_t cache_page_stride,
-                               const int32_t* block_table, int64_t bt_stride, const int32_t* cache_seqlens, void* out,
-                               int64_t o_sb, int64_t o_ss, int64_t o_sh, void* workspace, size_t workspace_bytes,
-                               int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv, int32_t head_dim,
-                               int32_t page_size, int32_t num_pages, int32_t max_blocks, int32_t causal,
-                               float softmax_scale, int32_t split_tokens, int32_t flags, int32_t* status,
-                               void* stream) {
-  using namespace pkv;
-  clear_error();
-  const char* fn = "pkv_decode_attn";
+namespace pkv {
+
+// The body of pkv_decode_attn.
+static int decode_attn(const char* fn, const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                       const void* k_new, int64_t kn_sb, int64_t kn_ss, int64_t kn_sh, const void* v_new,
+                       int64_t vn_sb, int64_t vn_ss, int64_t vn_sh, void* k_cache, void* v_cache,
+                       int64_t cache_page_stride, const int32_t* block_table, int64_t bt_stride,
+                       const int32_t* cache_seqlens, void* out, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+                       void* workspace, size_t workspace_bytes, int32_t batch, int32_t s_q, int32_t n_heads,
+                       int32_t n_kv, int32_t head_dim, int32_t page_size, int32_t num_pages, int32_t max_blocks,
+                       int32_t causal, float softmax_scale, int32_t split_tokens, int32_t flags, int32_t* status,
+                       void* stream) {
   int rc = validate_attn(fn, q, q_sb, q_ss, q_sh, k_new, kn_sb, kn_ss, kn_sh, v_new, vn_sb, vn_ss, vn_sh, k_cache,
                          v_cache, cache_page_stride, block_table, bt_stride, cache_seqlens, out, o_sb, o_ss, o_sh,
                          batch, s_q, n_heads, n_kv, head_dim, page_size, num_pages, max_blocks, softmax_scale);
@@ -2448,29 +2471,34 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
   if (ms > 65535) return fail(PKV_EINVAL, "%s: %lld splits exceed the grid limit", fn, (long long)ms);
   if (int64_t(batch) * n_kv * ms > (int64_t(1) << 30))
     return fail(PKV_EINVAL, "%s: %lld work items exceed the grid limit", fn, (long long)(int64_t(batch) * n_kv * ms));
+  if (!lean && ms > 1 && int64_t(batch) * n_kv > kMaxCounters)
+    return fail(PKV_EINVAL, "%s: batch * n_kv = %lld exceeds %d split-K counters; pass split_tokens >= "
+                "max_blocks * page_size", fn, (long long)batch * n_kv, kMaxCounters);
   if (batch == 0) return PKV_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int grid = lean ? lean_grid(flags) : 0;
+  const size_t need = lean ? ws_bytes_lean(grid, R) : (ms > 1 ? ws_bytes(batch, R, n_kv, head_dim, ms) : 0);
+  if (lean && need - kCounterBytes >= (size_t(1) << 31))
+    return fail(PKV_EINVAL, "%s: %d workgroups need a %zu-byte workspace (partials must stay under 2 GiB)",
+                fn, grid, need);
+  if (need > 0) {
+    if (!workspace || workspace_bytes < need)
+      return fail(PKV_ENOSPC, "%s: workspace %zu bytes < %zu needed", fn, workspace_bytes, need);
+    if (!aligned16(workspace)) return fail(PKV_EINVAL, "%s: workspace not 16-byte aligned", fn);
+  }
 
   AttnParams p;
   fill_params(p, q, q_sb, q_ss, q_sh, k_new, kn_sb, kn_ss, kn_sh, v_new, vn_sb, vn_ss, vn_sh, k_cache, v_cache,
               cache_page_stride, block_table, bt_stride, cache_seqlens, out, o_sb, o_ss, o_sh, s_q, n_heads, n_kv,
               page_size, num_pages, max_blocks, causal, softmax_scale, status);
   p.batch = batch;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   if (lean) {
     // balanced row-streaming kernel; partials merged by a second launch, or inside the launch
     // with PKV_DECODE_FUSED_MERGE (slower on the 7B decode step: the merge of a long sequence's
     // ~27 parts by its last range costs more than the second launch)
-    const int grid = lean_grid(flags);
-    const size_t need = ws_bytes_lean(grid, R);
-    if (need - kCounterBytes >= (size_t(1) << 31))
-      return fail(PKV_EINVAL, "%s: %d workgroups need a %zu-byte workspace (partials must stay under 2 GiB)",
-                  fn, grid, need);
-    if (!workspace || workspace_bytes < need)
-      return fail(PKV_ENOSPC, "%s: workspace %zu bytes < %zu needed", fn, workspace_bytes, need);
-    if (!aligned16(workspace)) return fail(PKV_EINVAL, "%s: workspace not 16-byte aligned", fn);
     p.ws_cnt = static_cast<int32_t*>(workspace);
     p.ws_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
-    p.ws_ml = p.ws_o + size_t(2) * grid * rows::NKV * R * rows::HD;
+    p.ws_ml = lean_lse_base(p.ws_o, size_t(2) * grid, R);
     p.two_pass = merge == PKV_DECODE_FUSED_MERGE ? 0 : 1;
     p.lean_grid = grid;
     switch ((R + 15) / 16) {
@@ -2488,13 +2516,6 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
   p.max_splits = int(ms);
   p.two_pass = merge == PKV_DECODE_TWO_PASS ? 1 : 0;
   if (ms > 1) {
-    const size_t need = ws_bytes(batch, R, n_kv, head_dim, ms);
-    if (!workspace || workspace_bytes < need)
-      return fail(PKV_ENOSPC, "%s: workspace %zu bytes < %zu needed", fn, workspace_bytes, need);
-    if (!aligned16(workspace)) return fail(PKV_EINVAL, "%s: workspace not 16-byte aligned", fn);
-    if (int64_t(batch) * n_kv > kMaxCounters)
-      return fail(PKV_EINVAL, "%s: batch * n_kv = %lld exceeds %d split-K counters; pass split_tokens >= "
-                  "max_blocks * page_size", fn, (long long)batch * n_kv, kMaxCounters);
     p.ws_cnt = static_cast<int32_t*>(workspace);
     p.ws_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
     p.ws_ml = p.ws_o + ws_floats_o(batch, R, n_kv, head_dim, ms);
@@ -2504,6 +2525,25 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
   else
     launch_decode_hd<64>(p, batch, s);
   return check_launch(fn);
+}
+
+}  // namespace pkv
+
+extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, const void* k_new,
+                               int64_t kn_sb, int64_t kn_ss, int64_t kn_sh, const void* v_new, int64_t vn_sb,
+                               int64_t vn_ss, int64_t vn_sh, void* k_cache, void* v_cache, int64_t cache_page_stride,
+                               const int32_t* block_table, int64_t bt_stride, const int32_t* cache_seqlens, void* out,
+                               int64_t o_sb, int64_t o_ss, int64_t o_sh, void* workspace, size_t workspace_bytes,
+                               int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv, int32_t head_dim,
+                               int32_t page_size, int32_t num_pages, int32_t max_blocks, int32_t causal,
+                               float softmax_scale, int32_t split_tokens, int32_t flags, int32_t* status,
+                               void* stream) {
+  pkv::clear_error();
+  return pkv::decode_attn("pkv_decode_attn", q, q_sb, q_ss, q_sh, k_new, kn_sb, kn_ss, kn_sh, v_new, vn_sb,
+                          vn_ss, vn_sh, k_cache, v_cache, cache_page_stride, block_table, bt_stride, cache_seqlens,
+                          out, o_sb, o_ss, o_sh, workspace, workspace_bytes, batch, s_q, n_heads, n_kv, head_dim,
+                          page_size, num_pages, max_blocks, causal, softmax_scale, split_tokens, flags, status,
+                          stream);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -2535,7 +2575,7 @@ static int cascade_splits_for(int batch, int R, int shared_tokens) {
 // sequence whose suffix one range holds whole.
 static size_t ws_bytes_cascade(int grid, int R, int batch, int S) {
   const size_t slots = size_t(2) * grid + size_t(batch) * (S + 1);
-  return kCounterBytes + slots * rows::NKV * R * (rows::HD + 2) * sizeof(float);
+  return kCounterBytes + slots * rows::NKV * R * kLeanRowBytes;
 }
 
 }  // namespace pkv
@@ -2593,7 +2633,7 @@ extern "C" int pkv_cascade_attn(const void* q, int64_t q_sb, int64_t q_ss, int64
   const size_t slots = size_t(2) * grid + size_t(batch) * (S + 1);
   p.ws_cnt = static_cast<int32_t*>(workspace);
   p.ws_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
-  p.ws_ml = p.ws_o + slots * rows::NKV * R * rows::HD;
+  p.ws_ml = lean_lse_base(p.ws_o, slots, R);
   p.two_pass = 1;
   p.lean_grid = grid;
   p.k0 = shared_tokens;

@@ -23,7 +23,10 @@ Deliberate differences (each fixes a defect of the reference or extends it):
     prepare_append copy it to a fresh page (copy-on-write, only the filled slots, every layer,
     K and V, one kernel launch for the whole batch);
   * build_block_table writes the whole [B, max_blocks] slice with one host-to-device copy (the
-    reference writes element by element, :147-151); columns past a sequence's pages are 0;
+    reference writes element by element, :147-151); columns past a sequence's pages are -1, so a
+    write through a column the sequence was never given (the reference executor's decode
+    capacity is one token short, engine/executor.py:206) is skipped and flagged
+    (PKV_STATUS_BAD_PAGE) instead of landing in page 0, the first page the allocator hands out;
   * transfer_sequence moves all pages of all layers with one kernel launch (the reference issues
     2 * L * pages copy_ calls, :189-207); migrate_to / compact move every live page (sequences
     and prefix-cache pages) into another pool, packed, rewriting page ids everywhere.
@@ -249,9 +252,9 @@ class FlashAttnKVCache:
 
     # ------------------------------------------------------------------ block tables
     def block_table_host(self, seq_ids: list[int]) -> tuple[np.ndarray, np.ndarray]:
-        """[B, max_blocks] int32 table (unused columns 0) and [B] int32 seq lengths, on the host."""
+        """[B, max_blocks] int32 table (unused columns -1) and [B] int32 seq lengths, on the host."""
         max_blocks = max(1, max(len(self.seq_pages.get(s, [1])) for s in seq_ids))
-        bt = np.zeros((len(seq_ids), max_blocks), dtype=np.int32)
+        bt = np.full((len(seq_ids), max_blocks), -1, dtype=np.int32)
         sl = np.empty(len(seq_ids), dtype=np.int32)
         for i, sid in enumerate(seq_ids):
             pages = self.seq_pages[sid]

@@ -186,7 +186,7 @@ def config4(device="cuda", seed=0, layers=None, max_pages=None, batch=8, chunk=5
 
 
 def config5(device="cuda", seed=0, layers=None, max_pages=None, batch=64, prefix=2048, max_suffix=1024,
-            draft=5, prefix_cache=None) -> PagedWorkload:
+            draft=5, prefix_cache=None, before_cow=None) -> PagedWorkload:
     """7B prefix sharing + speculative verify.
 
     A root sequence holds a shared prefix of 2048 - r tokens (r seeded in [1, 255], so the last
@@ -194,7 +194,8 @@ def config5(device="cuda", seed=0, layers=None, max_pages=None, batch=64, prefix
     given.  `batch` sequences fork the root (sharing all its pages), the root is freed, and each
     child grows by a private suffix ~ U{0..1024}: the first write into the shared boundary page
     copies it (one batched copy-on-write launch).  The step then verifies `draft` tokens per
-    sequence (s_q = 5, causal within the 5).
+    sequence (s_q = 5, causal within the 5).  before_cow(kv), when given, runs right before that
+    copy-on-write (a parity test snapshots the pool there).
     """
     s = SHAPES["7B"]
     L = layers or s["layers"]
@@ -211,17 +212,24 @@ def config5(device="cuda", seed=0, layers=None, max_pages=None, batch=64, prefix
     kv._ensure_capacity(root, shared)
     kv.seq_len[root] = shared
     if prefix_cache is not None:
+        # the cache cooperates with this pool: its pages stay off the free list while cached
+        prefix_cache.kv = kv
+        kv.prefix_cache = prefix_cache
         tokens = rng.integers(0, 150_000, size=shared).tolist()
         prefix_cache.store(tokens, kv.seq_pages[root], "target")
     ids = list(range(batch))
+    root_pages = list(kv.seq_pages[root])  # the prefix's pages, the last one partially filled
     for sid in ids:
         kv.fork_sequence(root, sid)
     kv.free_sequence(root)
     suffix = rng.integers(0, max_suffix + 1, size=batch)
+    if before_cow is not None:
+        before_cow(kv)
     n_cow = kv.prepare_append(ids, [int(x) for x in suffix])
     for sid, x in zip(ids, suffix):
         kv.seq_len[sid] += int(x)
     kv.prepare_append(ids, draft)
     ctx = np.array([kv.seq_len[sid] for sid in ids], dtype=np.int64)
     return _finish("config5", kv, ids, ctx, draft, s["n_heads"], g, device,
-                   {"shape": "7B", "shared_prefix": shared, "cow_copies": n_cow, "boundary_fill": shared % PAGE})
+                   {"shape": "7B", "shared_prefix": shared, "cow_copies": n_cow, "boundary_fill": shared % PAGE,
+                    "root_pages": root_pages})

@@ -107,3 +107,25 @@ def test_cascade_falls_back_off_page_boundaries(gpu):
                                                cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"],
                                                causal=True)
     assert_attn_close(out, ref, "cascade fallback")
+
+
+def test_cascade_without_append_checks_row_visibility(gpu):
+    # k = v = None, causal, s_q = 5: row 0 of a sequence with c keys sees keys [0, c - 5], so the
+    # prefix pass (which gives every row all shared keys) is right only when c >= shared + 4
+    cpu, dev, shared = _shared_case(gpu, suffix=[4, 40, 300], shared_pages=2, page_size=32, s_q=5)
+    out = torch.full_like(dev["q"], float("nan"))
+    prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], cache_seqlens=dev["cache_seqlens"],
+                                      block_table=dev["block_table"], causal=True, shared_prefix_tokens=shared,
+                                      out=out)
+    torch.cuda.synchronize()
+    assert prism_amd.read_status(gpu) == 0
+    ref, _, _ = pa.flash_attn_with_kvcache_ref(cpu["q"], cpu["k_cache"], cpu["v_cache"],
+                                               cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"],
+                                               causal=True)
+    assert_attn_close(out, ref, "cascade without append")
+    # a suffix of 3 keys: row 0 would wrongly see the last prefix key, so the call is flagged
+    cpu, dev, shared = _shared_case(gpu, suffix=[3, 40, 300], shared_pages=2, page_size=32, s_q=5)
+    prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], cache_seqlens=dev["cache_seqlens"],
+                                      block_table=dev["block_table"], causal=True, shared_prefix_tokens=shared)
+    torch.cuda.synchronize()
+    assert prism_amd.read_status(gpu) & prism_amd._lib.PKV_STATUS_SHARED_PREFIX

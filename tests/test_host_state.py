@@ -221,3 +221,28 @@ def test_random_operations_keep_pages_accounted(ops):
             _check_invariants(kv)
     finally:
         m.copy_pages = saved
+
+
+def test_unassigned_block_table_columns_never_name_a_live_page():
+    # A mixed batch where one sequence sits exactly on a page boundary.  The reference executor
+    # advances seq_len before building the table and grows capacity one token short
+    # (engine/executor.py:205-208, kv_cache.py:116-121), so its next append lands in the column
+    # after the sequence's last page.  That column must not hold a page anyone owns (the
+    # reference's zero would be page 0, the first page its allocator hands out, kv_cache.py:49).
+    from oracle.paged_attention import slot_mapping
+
+    kv = _kv(pages=16, P=16)
+    kv.new_sequence(0)
+    kv._ensure_capacity(0, 50)
+    kv.seq_len[0] = 49
+    kv.new_sequence(1)
+    kv.seq_len[1] = 16                        # exactly one full page, no room for token 16
+    bt, sl = kv.build_block_table([0, 1])
+    bt = bt.numpy()
+    assert bt[1].tolist() == [kv.seq_pages[1][0], -1, -1, -1]
+    assert bt[0, :4].tolist() == kv.seq_pages[0]
+    live = {p for pages in kv.seq_pages.values() for p in pages}
+    slots = slot_mapping(bt, sl.numpy(), 1, 16)
+    page_of = slots // 16
+    assert page_of[0, 0] in kv.seq_pages[0]
+    assert page_of[1, 0] < 0 and page_of[1, 0] not in live   # the kernels flag it and skip the write
