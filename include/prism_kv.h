@@ -137,6 +137,29 @@ int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
                     int32_t* status, void* stream);
 
 /*
+ * pkv_decode_attn without the workspace argument; it allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate or pass device memory for scratch (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  The split-K
+ * counters and partials live in the library's own static device array of 48 MiB, one per GPU,
+ * held until the process exits; a call that would need more (pkv_decode_workspace_bytes() >
+ * 48 MiB, e.g. more than ~64 KiB of counters plus 2 * #CU * 4 * R * 260 bytes on the balanced
+ * kernel) fails with PKV_ENOSPC before anything is launched.  Every call on a GPU shares that
+ * GPU's array: calls that overlap on one GPU (unordered streams) race.  The first call on a
+ * device looks the array up and clears its counters with a kernel on `stream`.  Same arguments
+ * (minus workspace), results and errors as pkv_decode_attn, bit for bit.
+ */
+int pkv_decode_attn_noalloc(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                            const void* k_new, int64_t kn_sb, int64_t kn_ss, int64_t kn_sh,
+                            const void* v_new, int64_t vn_sb, int64_t vn_ss, int64_t vn_sh,
+                            void* k_cache, void* v_cache, int64_t cache_page_stride,
+                            const int32_t* block_table, int64_t bt_stride, const int32_t* cache_seqlens,
+                            void* out, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+                            int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv, int32_t head_dim,
+                            int32_t page_size, int32_t num_pages, int32_t max_blocks,
+                            int32_t causal, float softmax_scale, int32_t split_tokens, int32_t flags,
+                            int32_t* status, void* stream);
+
+/*
  * Cascade (shared-prefix) attention: pkv_decode_attn for a batch whose sequences all list the
  * same pages for their first shared_tokens keys (branches of one prompt: the speculative verify
  * of engine/speculative_executor.py:113-164 over a cached prefix, engine/prefix_cache.py).

@@ -67,7 +67,7 @@ def read_status(device: torch.device | str = "cuda", clear: bool = True) -> int:
     return v
 
 
-def _workspace(device: torch.device, nbytes: int, stream: int) -> torch.Tensor | None:
+def _workspace(device: torch.device, nbytes: int, stream: int, allow_static: bool = False) -> torch.Tensor | None:
     """Split-K workspace per (device, stream), grow-only, allocated zero-filled: its counter
     region must start at zero, and every call leaves it zero again.
 
@@ -75,8 +75,10 @@ def _workspace(device: torch.device, nbytes: int, stream: int) -> torch.Tensor |
     then captures on a new one (engine/executor.py:186-197, :288-303), so a capture stream with
     no workspace of its own takes the largest one an eager call on this device sized; the graph's
     replays and the eager calls then share it, which is safe because Prism issues both from one
-    thread in order.  A workspace that grows is retired, never freed: a captured graph may still
-    hold its address."""
+    thread in order.  With allow_static, a capture that finds no sized workspace gets None: the
+    decode call then runs pkv_decode_attn_noalloc, whose scratch is the library's static device
+    array.  A workspace that grows is retired, never freed: a captured graph may still hold its
+    address."""
     if nbytes == 0:
         return None
     idx = device.index if device.index is not None else torch.cuda.current_device()
@@ -88,6 +90,8 @@ def _workspace(device: torch.device, nbytes: int, stream: int) -> torch.Tensor |
         if torch.cuda.is_current_stream_capturing():
             sized = [t for (d, _), t in _workspaces.items() if d == idx and t.numel() >= nbytes]
             if not sized:
+                if allow_static:
+                    return None   # the caller takes pkv_decode_attn_noalloc (the library's own scratch)
                 raise RuntimeError(
                     f"split-K workspace of {nbytes} bytes must be sized by an eager call on this device "
                     "before HIP graph capture")
@@ -199,6 +203,7 @@ def flash_attn_with_kvcache(
     kernel: str = "auto",
     grid: int = 0,
     shared_prefix_tokens: int = 0,
+    noalloc: bool = False,
     status: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Append k/v into the paged cache and attend (see module docstring for the contract).
@@ -218,6 +223,11 @@ def flash_attn_with_kvcache(
     cascade attention then reads that prefix once for the whole batch (pkv_cascade_attn).
     A sequence that breaks the promise sets PKV_STATUS_SHARED_PREFIX in the status word.
     Shapes the cascade does not cover run the ordinary decode path.
+
+    ``noalloc`` runs a decode / verify call on pkv_decode_attn_noalloc: its split-K scratch is the
+    library's static 48 MiB device array instead of a workspace this module allocates (calls on
+    one GPU then share that array and must be ordered).  A decode call under HIP graph capture
+    with no workspace sized by an earlier eager call takes the same path.
     """
     if rotary_cos is not None or rotary_sin is not None or cache_batch_idx is not None \
             or cache_leftpad is not None or tuple(window_size) != (-1, -1) or softcap != 0.0 \
@@ -295,7 +305,18 @@ def flash_attn_with_kvcache(
             return out
         nbytes = lib.pkv_decode_workspace_bytes(batch, s_q, n_heads, n_kv, hd, page_size, max_blocks,
                                                 int(split_tokens))
-        ws = _workspace(device, nbytes, stream)
+        ws = None if noalloc else _workspace(device, nbytes, stream, allow_static=True)
+        if noalloc or (ws is None and nbytes > 0):
+            rc = lib.pkv_decode_attn_noalloc(
+                q.data_ptr(), *qs, kp, *ks, vp, *vs,
+                k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
+                block_table.data_ptr(), block_table.stride(0), cache_seqlens.data_ptr(),
+                out.data_ptr(), *os_,
+                batch, s_q, n_heads, n_kv, hd, page_size, num_pages, max_blocks,
+                1 if causal else 0, scale, int(split_tokens), _decode_flags(two_pass, kernel, grid),
+                st.data_ptr(), stream)
+            _lib.check(rc, "pkv_decode_attn_noalloc")
+            return out
         rc = lib.pkv_decode_attn(
             q.data_ptr(), *qs, kp, *ks, vp, *vs,
             k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),

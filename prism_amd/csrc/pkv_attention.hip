@@ -23,6 +23,7 @@
 // Every K/V byte of a (sequence, KV head) is fetched once per query-row tile.
 #include <math.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "pkv_common.h"
@@ -2443,8 +2444,55 @@ extern "C" size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t
 
 namespace pkv {
 
-// The body of pkv_decode_attn.
-static int decode_attn(const char* fn, const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+// ---------------------------------------------------------------------------------------------
+// Static split-K scratch for pkv_decode_attn_noalloc, the allocation-free variant of
+// pkv_decode_attn: the arrival counters and partials live in this file-scope device array (each
+// GPU the library runs on holds its own copy, kScratchBytes, until the process exits).  Host code
+// never passes the array's name to a kernel or a copy: in host code it is a stand-in, not a
+// device address.  Its device address comes from hipGetSymbolAddress, once per device, with that
+// device current, and is kept per device.  Every call on a GPU shares that GPU's array, so calls
+// that overlap on one GPU (different streams, no ordering between them) race.
+// ---------------------------------------------------------------------------------------------
+constexpr size_t kScratchBytes = size_t(48) << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch[kMaxDevices];
+
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int n) {
+  for (int i = int(blockIdx.x) * 256 + int(threadIdx.x); i < n; i += int(gridDim.x) * 256) p[i] = 0u;
+}
+
+// Device address of the current device's scratch.  The first call on a device looks it up and
+// clears the counter region (a kernel on `stream`, not a memset, so that a first call under HIP
+// graph capture records an ordinary kernel node); every decode call leaves the counters at zero
+// again, and the partial regions are written before they are read within each call.
+static int scratch_for_current_device(const char* fn, hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(PKV_EHIP, "%s: hipGetDevice failed: %s", fn, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(PKV_EINVAL, "%s: device %d beyond %d", fn, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(PKV_EHIP, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", fn, dev,
+                  hipGetErrorString(e));
+    zero_words_kernel<<<int(kCounterBytes / 4 / 256), 256, 0, stream>>>(static_cast<uint32_t*>(ptr),
+                                                                         int(kCounterBytes / 4));
+    const int rc = check_launch(fn);
+    if (rc) return rc;
+    g_scratch[dev] = ptr;
+  }
+  *out = g_scratch[dev];
+  return PKV_OK;
+}
+
+// The body of pkv_decode_attn and pkv_decode_attn_noalloc.  With use_scratch the split-K
+// workspace is the static scratch (sizes beyond it are rejected before anything is launched);
+// otherwise the caller's.
+static int decode_attn(const char* fn, bool use_scratch, const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
                        const void* k_new, int64_t kn_sb, int64_t kn_ss, int64_t kn_sh, const void* v_new,
                        int64_t vn_sb, int64_t vn_ss, int64_t vn_sh, void* k_cache, void* v_cache,
                        int64_t cache_page_stride, const int32_t* block_table, int64_t bt_stride,
@@ -2481,6 +2529,13 @@ static int decode_attn(const char* fn, const void* q, int64_t q_sb, int64_t q_ss
   if (lean && need - kCounterBytes >= (size_t(1) << 31))
     return fail(PKV_EINVAL, "%s: %d workgroups need a %zu-byte workspace (partials must stay under 2 GiB)",
                 fn, grid, need);
+  if (use_scratch && need > 0) {
+    if (need > kScratchBytes)
+      return fail(PKV_ENOSPC, "%s: this call needs %zu bytes of split-K scratch, more than the library's "
+                  "%zu-byte static scratch; call pkv_decode_attn with a workspace", fn, need, kScratchBytes);
+    if ((rc = scratch_for_current_device(fn, s, &workspace))) return rc;
+    workspace_bytes = kScratchBytes;
+  }
   if (need > 0) {
     if (!workspace || workspace_bytes < need)
       return fail(PKV_ENOSPC, "%s: workspace %zu bytes < %zu needed", fn, workspace_bytes, need);
@@ -2539,9 +2594,26 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
                                float softmax_scale, int32_t split_tokens, int32_t flags, int32_t* status,
                                void* stream) {
   pkv::clear_error();
-  return pkv::decode_attn("pkv_decode_attn", q, q_sb, q_ss, q_sh, k_new, kn_sb, kn_ss, kn_sh, v_new, vn_sb,
+  return pkv::decode_attn("pkv_decode_attn", false, q, q_sb, q_ss, q_sh, k_new, kn_sb, kn_ss, kn_sh, v_new, vn_sb,
                           vn_ss, vn_sh, k_cache, v_cache, cache_page_stride, block_table, bt_stride, cache_seqlens,
                           out, o_sb, o_ss, o_sh, workspace, workspace_bytes, batch, s_q, n_heads, n_kv, head_dim,
+                          page_size, num_pages, max_blocks, causal, softmax_scale, split_tokens, flags, status,
+                          stream);
+}
+
+extern "C" int pkv_decode_attn_noalloc(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, const void* k_new,
+                                       int64_t kn_sb, int64_t kn_ss, int64_t kn_sh, const void* v_new, int64_t vn_sb,
+                                       int64_t vn_ss, int64_t vn_sh, void* k_cache, void* v_cache,
+                                       int64_t cache_page_stride, const int32_t* block_table, int64_t bt_stride,
+                                       const int32_t* cache_seqlens, void* out, int64_t o_sb, int64_t o_ss,
+                                       int64_t o_sh, int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv,
+                                       int32_t head_dim, int32_t page_size, int32_t num_pages, int32_t max_blocks,
+                                       int32_t causal, float softmax_scale, int32_t split_tokens, int32_t flags,
+                                       int32_t* status, void* stream) {
+  pkv::clear_error();
+  return pkv::decode_attn("pkv_decode_attn_noalloc", true, q, q_sb, q_ss, q_sh, k_new, kn_sb, kn_ss, kn_sh, v_new,
+                          vn_sb, vn_ss, vn_sh, k_cache, v_cache, cache_page_stride, block_table, bt_stride,
+                          cache_seqlens, out, o_sb, o_ss, o_sh, nullptr, 0, batch, s_q, n_heads, n_kv, head_dim,
                           page_size, num_pages, max_blocks, causal, softmax_scale, split_tokens, flags, status,
                           stream);
 }

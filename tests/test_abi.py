@@ -146,3 +146,35 @@ def test_ctypes_types_are_c_abi_only():
     for name, (res, args) in _lib._SIGNATURES.items():
         assert res in allowed, name
         assert all(a in allowed for a in args), name
+
+
+def _decode_noalloc(lib, **over):
+    a = dict(q=A16, q_sb=28 * 128, q_ss=28 * 128, q_sh=128, k=A16, k_sb=512, k_ss=512, k_sh=128,
+             v=A16, v_sb=512, v_ss=512, v_sh=128, kc=A16, vc=A16, page_stride=256 * 512, bt=A16, bt_stride=4,
+             sl=A16, out=A16, o_sb=28 * 128, o_ss=28 * 128, o_sh=128, batch=2, s_q=1, n_heads=28, n_kv=4,
+             head_dim=128, page_size=256, num_pages=10, max_blocks=4, causal=1, scale=0.088, split=0, flags=0)
+    a.update(over)
+    return lib.pkv_decode_attn_noalloc(a["q"], a["q_sb"], a["q_ss"], a["q_sh"], a["k"], a["k_sb"], a["k_ss"],
+                                       a["k_sh"], a["v"], a["v_sb"], a["v_ss"], a["v_sh"], a["kc"], a["vc"],
+                                       a["page_stride"], a["bt"], a["bt_stride"], a["sl"], a["out"], a["o_sb"],
+                                       a["o_ss"], a["o_sh"], a["batch"], a["s_q"], a["n_heads"], a["n_kv"],
+                                       a["head_dim"], a["page_size"], a["num_pages"], a["max_blocks"], a["causal"],
+                                       a["scale"], a["split"], a["flags"], None, None)
+
+
+def test_noalloc_rejects_before_any_device_work(lib):
+    # argument errors: the same checks as pkv_decode_attn, named for the variant
+    for over, msg in [(dict(head_dim=96, q_sh=96, k_sh=96, v_sh=96, o_sh=96), "head_dim"), (dict(s_q=10), "> 64"),
+                      (dict(flags=3), "bad flags"), (dict(split=48), "multiple of 32")]:
+        assert _decode_noalloc(lib, **over) == _lib.PKV_EINVAL
+        err = lib.pkv_last_error().decode()
+        assert "pkv_decode_attn_noalloc" in err and msg in err, err
+    # a call whose split-K partials exceed the 48 MiB static scratch: PKV_ENOSPC, with the size
+    over = dict(batch=256, n_kv=8, n_heads=64, k_sh=128, q_sh=128, q_sb=64 * 128, q_ss=64 * 128, o_sb=64 * 128,
+                o_ss=64 * 128, k_sb=1024, k_ss=1024, v_sb=1024, v_ss=1024, page_stride=256 * 1024, max_blocks=64,
+                bt_stride=64, split=256)
+    need = lib.pkv_decode_workspace_bytes(256, 1, 64, 8, 128, 256, 64, 256)
+    assert need > 48 << 20
+    assert _decode_noalloc(lib, **over) == _lib.PKV_ENOSPC
+    err = lib.pkv_last_error().decode()
+    assert "static scratch" in err and str(need) in err, err
