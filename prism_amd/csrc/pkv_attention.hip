@@ -1047,39 +1047,74 @@ __device__ __forceinline__ bool tile_has_new(const AttnParams& p, const TileDesc
   return p.has_new && d.T0 + rows::TILE > d.c && d.T0 < d.L;
 }
 
-// Copies of tile d into LDS buffer `buf`, 16 per wave: K then V rows of every head, wave w taking
-// rows w, w + 4, ..., lane l writing LDS chunk l of a row from global chunk l ^ swz(row).  A row
-// holding one of this call's new tokens (t >= c) is copied from k_new / v_new instead of the
-// cache, so attention sees it without waiting for the append.  When the tile starts a segment
-// (with_q), 4 more copies per wave bring the Q operand rows of head w into the buffer's Q area:
-// row r (clamped to R - 1) at [w][r], LDS chunk l holding global chunk l ^ (r & 15).
-template <int POLICY = rows::kStreamPolicy>
-__device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& d, bool with_q, char* buf,
-                                           int I0 = 0, int I1 = rows::TILE / rows::NKV) {
+// Per-lane byte offsets of a wave's row copies inside a tile's K (or V) rows: copy i of wave w is
+// token row r = 4 i + w, lane l reading global chunk l ^ swz(r) of the row into LDS chunk l.  The
+// same for every tile, so they are computed once per launch.
+struct RowOffsets {
+  uint32_t v[rows::TILE / rows::NKV];
+};
+
+__device__ __forceinline__ RowOffsets row_offsets() {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  RowOffsets ro;
+#pragma unroll
+  for (int i = 0; i < rows::TILE / rows::NKV; ++i) {
+    const int r = i * rows::NKV + wave;
+    ro.v[i] = uint32_t(r * rows::ROW_BYTES + ((lane ^ rows::swz(r)) << 4));
+  }
+  return ro;
+}
+
+// Copies of tile d into LDS buffer `buf`, 16 per wave: K then V rows of every head, wave w taking
+// rows w, w + 4, ..., lane l writing LDS chunk l of a row from global chunk l ^ swz(row).  A tile
+// without new rows is two buffers (its K rows and its V rows, 32 KiB each, base and range in
+// scalar registers) read at the precomputed lane offsets: one M0 write and one buffer load per
+// copy.  In a tile holding one of this call's new tokens (t >= c), that row's copy is sourced
+// from k_new / v_new instead of the cache, so attention sees it without waiting for the append.
+// When the tile starts a segment (with_q), 4 more copies per wave bring the Q operand rows of
+// head w into the buffer's Q area: row r (clamped to R - 1) at [w][r], LDS chunk l holding global
+// chunk l ^ (r & 15).
+template <int POLICY = rows::kStreamPolicy>
+__device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& d, bool with_q, char* buf,
+                                           const RowOffsets& ro, int I0 = 0, int I1 = rows::TILE / rows::NKV) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int64_t off = int64_t(d.pid < 0 ? 0 : d.pid) * p.page_stride +
                       int64_t(d.T0 & ((1 << p.log2_page) - 1)) * (rows::NKV * rows::HD);
-  const char* kg = uniform_ptr(reinterpret_cast<const char*>(p.k_cache + off));
-  const char* vg = uniform_ptr(reinterpret_cast<const char*>(p.v_cache + off));
-  const bool any_new = tile_has_new(p, d);
+  if (!tile_has_new(p, d)) {
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(p.k_cache + off), 0, rows::TILE_BYTES, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(p.v_cache + off), 0, rows::TILE_BYTES, 0x00020000);
 #pragma unroll
-  for (int i = I0; i < I1; ++i) {
-    const int r = i * rows::NKV + wave;
-    const int t = d.T0 + r;
-    const uint32_t gc = uint32_t(lane ^ rows::swz(r));
-    const char* ks = kg + (r * rows::ROW_BYTES + (gc << 4));
-    const char* vs = vg + (r * rows::ROW_BYTES + (gc << 4));
-    if (any_new && t >= d.c && t < d.L) {
-      const int jn = t - d.c;
-      const int hh = int(gc >> 4);
-      const int w8 = int(gc & 15) * 8;
-      ks = reinterpret_cast<const char*>(p.k_new + d.b * p.kn_sb + jn * p.kn_ss + hh * p.kn_sh + w8);
-      vs = reinterpret_cast<const char*>(p.v_new + d.b * p.vn_sb + jn * p.vn_ss + hh * p.vn_sh + w8);
+    for (int i = I0; i < I1; ++i) {
+      char* dst = buf + (i * rows::NKV + wave) * rows::ROW_BYTES;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (rows::lds_void*)dst, 16, int(ro.v[i]), 0, 0, POLICY);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (rows::lds_void*)(dst + rows::TILE_BYTES), 16, int(ro.v[i]), 0,
+                                               0, POLICY);
     }
-    __builtin_amdgcn_global_load_lds(ks, (rows::lds_void*)(buf + r * rows::ROW_BYTES), 16, 0, POLICY);
-    __builtin_amdgcn_global_load_lds(vs, (rows::lds_void*)(buf + rows::TILE_BYTES + r * rows::ROW_BYTES), 16, 0,
-                                     POLICY);
+  } else {
+    const char* kg = uniform_ptr(reinterpret_cast<const char*>(p.k_cache + off));
+    const char* vg = uniform_ptr(reinterpret_cast<const char*>(p.v_cache + off));
+#pragma unroll
+    for (int i = I0; i < I1; ++i) {
+      const int r = i * rows::NKV + wave;
+      const int t = d.T0 + r;
+      const uint32_t gc = uint32_t(lane ^ rows::swz(r));
+      const char* ks = kg + (r * rows::ROW_BYTES + (gc << 4));
+      const char* vs = vg + (r * rows::ROW_BYTES + (gc << 4));
+      if (t >= d.c && t < d.L) {
+        const int jn = t - d.c;
+        const int hh = int(gc >> 4);
+        const int w8 = int(gc & 15) * 8;
+        ks = reinterpret_cast<const char*>(p.k_new + d.b * p.kn_sb + jn * p.kn_ss + hh * p.kn_sh + w8);
+        vs = reinterpret_cast<const char*>(p.v_new + d.b * p.vn_sb + jn * p.vn_ss + hh * p.vn_sh + w8);
+      }
+      __builtin_amdgcn_global_load_lds(ks, (rows::lds_void*)(buf + r * rows::ROW_BYTES), 16, 0, POLICY);
+      __builtin_amdgcn_global_load_lds(vs, (rows::lds_void*)(buf + rows::TILE_BYTES + r * rows::ROW_BYTES), 16, 0,
+                                       POLICY);
+    }
   }
   if (with_q) {
 #pragma unroll
@@ -1271,93 +1306,138 @@ __device__ __forceinline__ void unpack_f16x8(const u32x4 v, float (&f)[8]) {
   }
 }
 
-// Log-sum-exp merge of the np partials of (b, KV head h) into the bf16 output, by one wave.
-// The code stays small on purpose: it runs once per launch, from a cold instruction cache, so a
-// fully unrolled merge spends microseconds fetching instructions.  Parts come into this wave's
-// LDS area by global->LDS DMA issued from a loop (no register staging, every copy of a batch in
-// flight at once); lane r < R then keeps row r's running max and weight sum, and lane l
-// accumulates float-16 chunks i = 64c + l (row i / 16, head-dim 8 (i % 16)) over the parts.
-// Area layout: [0, 512) per-row rescale and 1 / sum | KB part blocks of R x head_dim fp16 | their
-// log-sum-exps, overwritten by the weights.
+// Log-sum-exp merge of the np partials of (b, KV head h) into the bf16 output, by one wave, with
+// the parts read straight from the workspace into registers (device-coherent buffer loads).
+// Lane l owns the 16-byte chunks i = l + 64 c (c < NC) of the R x head_dim block: row i / 16,
+// head-dim elements 8 (i % 16) .. + 7.  Parts go in windows of at most KW (as many as the LDS
+// area holds log-sum-exps for; one window unless np * R is in the thousands):
+//   1. every lane loads some of the window's log-sum-exps into the area, row-major [r][k];
+//   2. lane r < R turns row r's into weights exp2(lse - M) against the running max M, rescales
+//      the running sum and publishes the factor that rescales what was accumulated so far;
+//   3. every lane accumulates its chunks over the window's parts, PB parts per batch, the next
+//      batch's loads in flight during this one's FMAs (2 PB NC 16-byte loads outstanding per
+//      lane at most: beyond ~24 the latency of such loads rises tenfold).
+// No loop body reads LDS in a dependent chain: a lane's weights come four at a time.
 template <int NC>
-__device__ __forceinline__ void merge_parts(const AttnParams& p, int b, int h, const SeqParts& sp, char* area,
-                                            int area_bytes) {
+__device__ __forceinline__ void merge_parts(const AttnParams& p, int b, int h, const SeqParts& sp, float* area,
+                                            int area_floats) {
   constexpr int HD = rows::HD;
+  constexpr int PB = NC >= 8 ? 1 : 8 / NC;
   const int lane = threadIdx.x & 63;
   const int R = p.R;
-  const int part_bytes = R * HD * 2;
   const int nch = R * (HD / 8);
-  float* stat = reinterpret_cast<float*>(area);
-  char* oarea = area + 512;
-  const int KB = min(32, (area_bytes - 512) / (part_bytes + 4 * R));
-  float* lsea = reinterpret_cast<float*>(oarea + KB * part_bytes);
-  const char* ws_o = reinterpret_cast<const char*>(p.ws_o);
+  // weights [r][k] with a row pitch KWP (a multiple of 4), then per-row rescale and 1 / sum
+  const int KWP = min(((sp.np + 3) & ~3), ((area_floats - 2 * R) / R) & ~3);
+  float* wts = area;
+  float* resc = area + R * KWP;
+  float* rinv = resc + R;
+  const __amdgpu_buffer_rsrc_t rs = ws_rsrc(p);
+  const uint32_t lse0 = uint32_t(p.ws_ml - p.ws_o) * 4u;
+  auto part_row0 = [&](int k) -> uint32_t {
+    const int slot = k == 0 ? sp.slot0 : 2 * (sp.w0 + k);
+    return uint32_t((slot * rows::NKV + h) * R);
+  };
+  int rowc[NC];
+  bool okc[NC];
   float acc[NC][8];
 #pragma unroll
-  for (int c = 0; c < NC; ++c)
+  for (int c = 0; c < NC; ++c) {
+    const int i = lane + 64 * c;
+    okc[c] = i < nch;
+    rowc[c] = (okc[c] ? i : 0) >> 4;
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[c][e] = 0.f;
-  float M = -INFINITY, S = 0.f;
-  for (int u0 = 0; u0 < sp.np; u0 += KB) {
-    const int nb = min(KB, sp.np - u0);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the previous batch is no longer read
-#pragma unroll 1
-    for (int k = 0; k < nb; ++k) {
-      const int part = u0 + k;
-      const int rb = ((part == 0 ? sp.slot0 : 2 * (sp.w0 + part)) * rows::NKV + h) * R;
-      const char* src = ws_o + int64_t(rb) * (HD * 2);
-#pragma unroll 1
-      for (int q = 0; q * 1024 < part_bytes; ++q)
-        if (q * 1024 + 16 * lane < part_bytes)
-          __builtin_amdgcn_global_load_lds(src + q * 1024 + 16 * lane, (rows::lds_void*)(oarea + k * part_bytes + q * 1024),
-                                           16, 0, kCoherent);
-      if (lane < R)
-        __builtin_amdgcn_global_load_lds(p.ws_ml + rb + lane, (rows::lds_void*)(lsea + k * R), 4, 0, kCoherent);
+  }
+  float M = -INFINITY, S = 0.f;  // lanes r < R: row r's running max and sum of weights
+  for (int k0 = 0; k0 < sp.np; k0 += KWP) {
+    const int nk = min(KWP, sp.np - k0);
+    // 1. log-sum-exps, -inf past the window's parts
+    for (int e = lane; e < R * KWP; e += 64) {
+      const int r = e / KWP;
+      const int k = e - r * KWP;
+      float v = -INFINITY;
+      if (k < nk)
+        v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                          rs, int(lse0 + (part_row0(k0 + k) + r) * 4u), 0, kCoherent));
+      wts[e] = v;
     }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the batch is in LDS
+    // 2. weights (this wave's own LDS writes complete before its later LDS reads)
     if (lane < R) {
+      float* wr = wts + lane * KWP;
       float Mn = M;
-#pragma unroll 1
-      for (int k = 0; k < nb; ++k) Mn = fmaxf(Mn, lsea[k * R + lane]);
-      const float Mu = Mn == -INFINITY ? 0.f : Mn;
-      const float resc = fast_exp2(M - Mu);
-      S *= resc;
-#pragma unroll 1
-      for (int k = 0; k < nb; ++k) {
-        const float w = fast_exp2(lsea[k * R + lane] - Mu);
-        S += w;
-        lsea[k * R + lane] = w;
+      for (int k = 0; k < nk; k += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(wr + k);
+        Mn = fmaxf(Mn, fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
       }
-      stat[lane] = resc;
+      const float Mu = Mn == -INFINITY ? 0.f : Mn;
+      const float f = fast_exp2(M - Mu);  // 0 while nothing was accumulated (M = -inf)
+      S *= f;
+      for (int k = 0; k < nk; k += 4) {
+        f32x4 v = *reinterpret_cast<const f32x4*>(wr + k);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          v[q] = fast_exp2(v[q] - Mu);
+          S += v[q];
+        }
+        *reinterpret_cast<f32x4*>(wr + k) = v;
+      }
+      resc[lane] = f;
       M = Mn;
     }
-    // the weights were written by this wave's own lanes: its LDS operations complete in order
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int i = 64 * c + lane;
-      if (i < nch) {
-        const int row = i >> 4;
-        const float rs_ = stat[row];
+      const float f = resc[rowc[c]];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[c][e] *= rs_;
-#pragma unroll 1
-        for (int k = 0; k < nb; ++k) {
-          const float w = lsea[k * R + row];
-          float f[8];
-          unpack_f16x8(*reinterpret_cast<const u32x4*>(oarea + k * part_bytes + 16 * i), f);
+      for (int e = 0; e < 8; ++e) acc[c][e] *= f;
+    }
+    // 3. the window's parts
+    u32x4 xa[PB][NC], xb[PB][NC];
+    auto load = [&](u32x4 (&x)[PB][NC], int kb) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[c][e] += w * f[e];
+      for (int kk = 0; kk < PB; ++kk) {
+        const int k = kb + kk;
+        const uint32_t base = part_row0(k0 + (k < nk ? k : 0)) * uint32_t(HD * 2);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          x[kk][c] = u32x4{0u, 0u, 0u, 0u};
+          if (k < nk && okc[c])
+            x[kk][c] = __builtin_amdgcn_raw_buffer_load_b128(rs, int(base + uint32_t(lane + 64 * c) * 16u), 0,
+                                                             kCoherent);
         }
       }
+    };
+    auto accum = [&](const u32x4 (&x)[PB][NC], int kb) {
+#pragma unroll
+      for (int kk = 0; kk < PB; ++kk) {
+        const int k = kb + kk;
+        if (k < nk) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const float wt = wts[rowc[c] * KWP + k];
+            float f[8];
+            unpack_f16x8(x[kk][c], f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[c][e] += wt * f[e];
+          }
+        }
+      }
+    };
+    load(xa, 0);
+    for (int kb = 0; kb < nk; kb += 2 * PB) {
+      if (kb + PB < nk) load(xb, kb + PB);
+      accum(xa, kb);
+      if (kb + PB >= nk) break;
+      if (kb + 2 * PB < nk) load(xa, kb + 2 * PB);
+      accum(xb, kb + PB);
     }
   }
-  if (lane < R) stat[64 + lane] = S > 0.f ? 1.f / S : 0.f;
+  if (lane < R) rinv[lane] = S > 0.f ? 1.f / S : 0.f;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    const int i = 64 * c + lane;
-    if (i < nch) {
-      const int row = i >> 4;
-      const float inv = stat[64 + row];
+    if (okc[c]) {
+      const int i = lane + 64 * c;
+      const int row = rowc[c];
+      const float inv = rinv[row];
       const int j = row / p.g;
       const int hq = row - j * p.g;
       u32x4 ov;
@@ -1368,17 +1448,19 @@ __device__ __forceinline__ void merge_parts(const AttnParams& p, int b, int h, c
   }
 }
 
-// merge_parts for the row count of the launch (chunks per lane: R * 16 / 64).
+// merge_parts for the row count of the launch (chunks per lane: R * 16 / 64, rounded up).
 template <int NT>
-__device__ __forceinline__ void merge_parts_for(const AttnParams& p, int b, int h, const SeqParts& sp, char* area,
-                                                int area_bytes) {
+__device__ __forceinline__ void merge_parts_for(const AttnParams& p, int b, int h, const SeqParts& sp, float* area,
+                                                int area_floats) {
   if constexpr (NT == 1) {
-    if (p.R <= 8)
-      merge_parts<2>(p, b, h, sp, area, area_bytes);
+    if (p.R <= 4)
+      merge_parts<1>(p, b, h, sp, area, area_floats);
+    else if (p.R <= 8)
+      merge_parts<2>(p, b, h, sp, area, area_floats);
     else
-      merge_parts<4>(p, b, h, sp, area, area_bytes);
+      merge_parts<4>(p, b, h, sp, area, area_floats);
   } else {
-    merge_parts<4 * NT>(p, b, h, sp, area, area_bytes);
+    merge_parts<4 * NT>(p, b, h, sp, area, area_floats);
   }
 }
 
@@ -1408,10 +1490,11 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   tile_window(p, st, s, e, win);
   TileDesc dA = tile_desc(win, s);
   TileDesc dB = dA;
-  rows_issue<kPolicy>(p, dA, kQInLds, lds);
+  const RowOffsets ro = row_offsets();
+  rows_issue<kPolicy>(p, dA, kQInLds, lds, ro);
   if (n > 1) {
     dB = tile_desc(win, s + 1);
-    rows_issue<kPolicy>(p, dB, kQInLds && dB.T0 == p.k0, lds + BUF);
+    rows_issue<kPolicy>(p, dB, kQInLds && dB.T0 == p.k0, lds + BUF, ro);
   }
 
   bf16x8 qf[NT][HD / 32];
@@ -1488,7 +1571,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
       const int x2 = s + j + 2;
       if (x2 - win.x0 >= 64) tile_window(p, st, x2, e, win);
       d2 = tile_desc(win, x2);
-      rows_issue<kPolicy>(p, d2, false, buf, 0, 4);
+      rows_issue<kPolicy>(p, d2, false, buf, ro, 0, 4);
     }
     dA = dB;
     dB = d2;
@@ -1500,7 +1583,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
       else
         compute_tile<HD, NT, true>(p, tl, d.T0, qf, lim, lim_min, m_run, l_run, acc);
     }
-    if (next2) rows_issue<kPolicy>(p, d2, kQInLds && d2.T0 == p.k0, buf, 4, 8);
+    if (next2) rows_issue<kPolicy>(p, d2, kQInLds && d2.T0 == p.k0, buf, ro, 4, 8);
 
     stores_prev2 = stores_prev;
     stores_prev = 0;
@@ -1581,7 +1664,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   // count merges every part and re-arms the counter for the next call.  Nobody waits.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the partial stores are device-visible
   // the tile buffers are free after the loop: a quarter of them per wave for its merges
-  char* area = lds + h * (2 * BUF / rows::NKV);
+  float* area = reinterpret_cast<float*>(lds + h * (2 * BUF / rows::NKV));
   // both arrivals in flight together, then the merges this wave completes
   int prev0 = 0, prev1 = 0;
   if (lane == 0) {
@@ -1601,7 +1684,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     const SeqParts sp = seq_parts(p, st, b, per);
     if ((k == 0 ? prev0 : prev1) != sp.np - 1) continue;
     if (lane == 0) __hip_atomic_store(p.ws_cnt + b * rows::NKV + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_parts_for<NT>(p, b, h, sp, area, 2 * BUF / rows::NKV);
+    merge_parts_for<NT>(p, b, h, sp, area, 2 * BUF / rows::NKV / 4);
   }
 }
 
@@ -1624,34 +1707,50 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // Two-pass merge (PKV_DECODE_TWO_PASS) of the partials a decode_lean_kernel launch of `grid`
 // workgroups left in the workspace.  Workgroup (KV head, sequence, group of 16 query rows), one
-// wave per query row; only sequences whose tiles span more than one range have partials.  Lane
-// u holds part u's log-sum-exp; lane l owns head-dim elements 2l and 2l + 1 and reads them from
-// every part, all loads of a batch of 32 parts in flight at once; the parts' weights reach every
-// lane by v_readlane.  No LDS, no barrier.
-constexpr int kLeanMergeBatch = 32;
+// wave per query row; only sequences whose tiles span more than one range have partials.  The
+// merge is latency-bound, so everything one round trip can fetch is fetched at once, for up to
+// 64 parts: lane u loads part u's log-sum-exp, and lane (g, c) = (lane / 16, lane % 16) loads the
+// 16 bytes of head-dim chunk c (elements 8c .. 8c + 7) of parts g, g + 4, ..., g + 60 of its row
+// (16 loads in flight per lane: one round trip for 64 parts, where 4-byte loads needed one per 8).
+// Weights reach the lanes by ds_bpermute, the four part groups are summed with the row-swap
+// permutes, and lanes of group 0 store the row.  No LDS, no barrier; loops stay rolled where the
+// code would otherwise grow (every launch starts from a cold instruction cache).
+constexpr int kLeanMergeParts = 64;
 
 __global__ __launch_bounds__(1024) void combine_lean_kernel(const AttnParams p, int grid) {
   constexpr int HD = rows::HD;
+  static_assert(HD == 128, "16 lanes x 16 bytes per part row");
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int r = int(blockIdx.z) * 16 + int(threadIdx.x >> 6);  // query row of this wave
   const int lane = threadIdx.x & 63;
   if (r >= p.R) return;
 
-  SeqTable st;
-  seq_table(p, st);
-  const int per = (st.total + grid - 1) / grid;
-  int first = 0, L = 0;
-#pragma unroll
-  for (int q = 0; q < rows::kChunks; ++q) {
-    if (q == (b >> 6)) {
-      first = __builtin_amdgcn_readlane(st.first[q], b & 63);
-      L = __builtin_amdgcn_readlane(st.L[q], b & 63);
+  // first tile and key count of sequence b and the tiles of all sequences: the prefix sum of
+  // seq_table (same clamp), one 64-sequence chunk at a time
+  const int cap = p.max_blocks << p.log2_page;
+  const int s_new = p.has_new ? p.s_q : 0;
+  int first = 0, L = 0, total = 0;
+#pragma unroll 1
+  for (int q0 = 0; q0 < p.batch; q0 += 64) {
+    const int bb = q0 + lane;
+    int c = bb < p.batch ? p.seqlens[bb] : 0;
+    int Lb = c + s_new;
+    if (c < 0 || Lb > cap) {
+      c = min(max(c, 0), cap);
+      Lb = min(c + s_new, cap);
     }
+    const int n = bb < p.batch ? seq_tiles(p, Lb) : 0;
+    const int incl = total + wave_incl_scan(n);
+    if (b >= q0 && b < q0 + 64) {
+      first = __builtin_amdgcn_readlane(incl - n, b - q0);
+      L = __builtin_amdgcn_readlane(Lb, b - q0);
+    }
+    total = __builtin_amdgcn_readlane(incl, 63);
   }
+  const int per = (total + grid - 1) / grid;
   const int w0 = first / per;
-  const int w1 = (first + seq_tiles(p, L) - 1) / per;
-  const int np = w1 - w0 + 1;
+  const int np = (first + seq_tiles(p, L) - 1) / per - w0 + 1;
   // cascade: the prefix pass's S parts first, then the sequence's suffix partial(s)
   const int S = p.cascade_splits;
   if (np <= 1 && S == 0) return;
@@ -1668,40 +1767,59 @@ __global__ __launch_bounds__(1024) void combine_lean_kernel(const AttnParams p, 
     }
     return (int64_t(slot) * rows::NKV + h) * p.R + r;
   };
-  const uint32_t* o16 = reinterpret_cast<const uint32_t*>(p.ws_o);  // fp16 pairs
+  const int pg = lane >> 4;
+  const int dc = lane & 15;
+  const char* o16 = reinterpret_cast<const char*>(p.ws_o);  // fp16 rows of HD * 2 bytes
   float M_run = -INFINITY, S_run = 0.f;
-  f32x2 o = {0.f, 0.f};
-  for (int u0 = 0; u0 < n_parts; u0 += kLeanMergeBatch) {
-    const int nb = min(kLeanMergeBatch, n_parts - u0);
-    uint32_t x[kLeanMergeBatch];
+  float acc[8];
 #pragma unroll
-    for (int k = 0; k < kLeanMergeBatch; ++k) {
-      x[k] = 0u;
-      if (k < nb) x[k] = o16[row_of(u0 + k) * (HD / 2) + lane];
-    }
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  // parts u0 .. u0 + nb - 1 (nb <= 4 KP): every load at once, then the weights and the sums
+  auto batch = [&](auto kp, int u0, int nb) {
+    constexpr int KP = decltype(kp)::value;
     const float lse = lane < nb ? p.ws_ml[row_of(u0 + lane)] : -INFINITY;
+    u32x4 x[KP];
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+      const int part = 4 * k + pg;
+      x[k] = u32x4{0u, 0u, 0u, 0u};
+      if (part < nb) x[k] = ld16(o16 + row_of(u0 + part) * (HD * 2) + dc * 16);
+    }
     const float M_new = fmaxf(M_run, wave_max(lse));
     const float M_use = (M_new == -INFINITY) ? 0.f : M_new;
-    const float w = fast_exp2(lse - M_use);
+    const float w = fast_exp2(lse - M_use);  // 0 for lanes past the batch
     const float resc = fast_exp2(M_run - M_use);
     S_run = S_run * resc + wave_sum(w);
     M_run = M_new;
-    o *= resc;
 #pragma unroll
-    for (int k = 0; k < kLeanMergeBatch; ++k) {
-      if (k < nb) {
-        const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), k));
-        const _Float16 lo = __builtin_bit_cast(_Float16, uint16_t(x[k] & 0xffffu));
-        const _Float16 hi = __builtin_bit_cast(_Float16, uint16_t(x[k] >> 16));
-        o += wk * f32x2{float(lo), float(hi)};
-      }
+    for (int e = 0; e < 8; ++e) acc[e] *= resc;
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+      const float wk = __shfl(w, 4 * k + pg, 64);
+      float f[8];
+      unpack_f16x8(x[k], f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += wk * f[e];
     }
+  };
+  if (n_parts <= 8) {
+    batch(std::integral_constant<int, 2>(), 0, n_parts);
+  } else {
+#pragma unroll 1
+    for (int u0 = 0; u0 < n_parts; u0 += kLeanMergeParts)
+      batch(std::integral_constant<int, kLeanMergeParts / 4>(), u0, min(kLeanMergeParts, n_parts - u0));
   }
-  const float inv = S_run > 0.f ? 1.f / S_run : 0.f;
-  const int j = r / p.g;
-  const int hq = r - j * p.g;
-  *reinterpret_cast<uint32_t*>(p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + 2 * lane) =
-      pack_bf16x2(o[0] * inv, o[1] * inv);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = sum_over_quads(acc[e]);
+  if (pg == 0) {
+    const float inv = S_run > 0.f ? 1.f / S_run : 0.f;
+    const int j = r / p.g;
+    const int hq = r - j * p.g;
+    u32x4 ov;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[2 * k] * inv, acc[2 * k + 1] * inv);
+    st16(p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + 8 * dc, ov);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
