@@ -933,26 +933,28 @@ __device__ __forceinline__ int seq_tiles(const AttnParams& p, int L) {
 
 // Every sequence's clamped lengths and first tile, 64 sequences per register (lane l of register
 // q holds sequence 64q + l), from one read of cache_seqlens per wave.  The clamp is seq_lengths'.
+template <int NCH>
 struct SeqTable {
-  int c[rows::kChunks], L[rows::kChunks], first[rows::kChunks];
-  int end[rows::kChunks];  // uniform: one past the last tile of chunk q
+  int c[NCH], L[NCH], first[NCH];
+  int end[NCH];  // uniform: one past the last tile of chunk q
   int total;               // T, tiles over all sequences
 };
 
-__device__ __forceinline__ void seq_table(const AttnParams& p, SeqTable& st) {
+template <int NCH>
+__device__ __forceinline__ void seq_table(const AttnParams& p, SeqTable<NCH>& st) {
   const int lane = threadIdx.x & 63;
   const int cap = p.max_blocks << p.log2_page;
   const int s_new = p.has_new ? p.s_q : 0;
-  int raw[rows::kChunks];
+  int raw[NCH];
 #pragma unroll
-  for (int q = 0; q < rows::kChunks; ++q) {
+  for (int q = 0; q < NCH; ++q) {
     const int b = 64 * q + lane;
     raw[q] = 0;
     if (64 * q < p.batch && b < p.batch) raw[q] = p.seqlens[b];
   }
   int base = 0;
 #pragma unroll
-  for (int q = 0; q < rows::kChunks; ++q) {
+  for (int q = 0; q < NCH; ++q) {
     const int b = 64 * q + lane;
     int c = raw[q];
     int L = c + s_new;
@@ -974,14 +976,15 @@ __device__ __forceinline__ void seq_table(const AttnParams& p, SeqTable& st) {
 
 // Sequence of tile x (per lane, x < total): its index, first tile and lengths.  A binary search
 // over the chunk's first tiles (non-decreasing across lanes) with lane permutes.
-__device__ __forceinline__ void locate_tile(const AttnParams& p, const SeqTable& st, int x, int& b, int& first,
+template <int NCH>
+__device__ __forceinline__ void locate_tile(const AttnParams& p, const SeqTable<NCH>& st, int x, int& b, int& first,
                                             int& c, int& L) {
   b = 0;
   first = 0;
   c = 0;
   L = 0;
 #pragma unroll
-  for (int q = 0; q < rows::kChunks; ++q) {
+  for (int q = 0; q < NCH; ++q) {
     if (64 * q >= p.batch) break;
     int pos = 0;
 #pragma unroll
@@ -1013,7 +1016,8 @@ struct TileDesc {
   int b, T0, c, L, pid;
 };
 
-__device__ __forceinline__ void tile_window(const AttnParams& p, const SeqTable& st, int x0, int e, TileWin& w) {
+template <int NCH>
+__device__ __forceinline__ void tile_window(const AttnParams& p, const SeqTable<NCH>& st, int x0, int e, TileWin& w) {
   const int lane = threadIdx.x & 63;
   const int x = min(x0 + lane, e - 1);
   int b, first, c, L;
@@ -1082,7 +1086,7 @@ __device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& 
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int64_t off = int64_t(d.pid < 0 ? 0 : d.pid) * p.page_stride +
                       int64_t(d.T0 & ((1 << p.log2_page) - 1)) * (rows::NKV * rows::HD);
-  if (!tile_has_new(p, d)) {
+  if (__builtin_expect(!tile_has_new(p, d), 1)) {
     const __amdgpu_buffer_rsrc_t rk =
         __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(p.k_cache + off), 0, rows::TILE_BYTES, 0x00020000);
     const __amdgpu_buffer_rsrc_t rv =
@@ -1266,10 +1270,11 @@ struct SeqParts {
   int np, w0, slot0;
 };
 
-__device__ __forceinline__ SeqParts seq_parts(const AttnParams& p, const SeqTable& st, int b, int per) {
+template <int NCH>
+__device__ __forceinline__ SeqParts seq_parts(const AttnParams& p, const SeqTable<NCH>& st, int b, int per) {
   int first = 0, L = 0;
 #pragma unroll
-  for (int q = 0; q < rows::kChunks; ++q) {
+  for (int q = 0; q < NCH; ++q) {
     if (q == (b >> 6)) {
       first = __builtin_amdgcn_readlane(st.first[q], b & 63);
       L = __builtin_amdgcn_readlane(st.L[q], b & 63);
@@ -1464,7 +1469,7 @@ __device__ __forceinline__ void merge_parts_for(const AttnParams& p, int b, int 
   }
 }
 
-template <int NT>
+template <int NT, int NCH>
 __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p) {
   constexpr int HD = rows::HD;
   constexpr int DPL = HD / 16;
@@ -1478,7 +1483,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   const int li = lane & 15;
   const int lq = lane >> 4;
 
-  SeqTable st;
+  SeqTable<NCH> st;
   seq_table(p, st);
   const int per = (st.total + int(gridDim.x) - 1) / int(gridDim.x);
   const int s = min(int(blockIdx.x) * per, st.total);
@@ -2410,6 +2415,25 @@ static int lean_grid(int32_t flags) {
   return g > 0 ? g : device_cu_count();
 }
 
+// decode_lean_kernel for R query rows per KV head (NT = R / 16 MFMA row tiles, rounded up) and
+// a batch of up to 64 or up to 256 sequences (the sequence table's register chunks: a kernel for
+// small batches carries a quarter of the scan and search code, which every launch fetches cold).
+template <int NT>
+static void launch_lean_nt(const AttnParams& p, int batch, int grid, hipStream_t s) {
+  if (batch <= 64)
+    decode_lean_kernel<NT, 1><<<grid, 64 * rows::NKV, 0, s>>>(p);
+  else
+    decode_lean_kernel<NT, rows::kChunks><<<grid, 64 * rows::NKV, 0, s>>>(p);
+}
+static void launch_lean(const AttnParams& p, int R, int batch, int grid, hipStream_t s) {
+  switch ((R + 15) / 16) {
+    case 1: launch_lean_nt<1>(p, batch, grid, s); break;
+    case 2: launch_lean_nt<2>(p, batch, grid, s); break;
+    case 3: launch_lean_nt<3>(p, batch, grid, s); break;
+    default: launch_lean_nt<4>(p, batch, grid, s); break;
+  }
+}
+
 // Same counter region | partial O / l [2 grid, n_kv, R, head_dim] fp16 | log-sum-exp
 // [2 grid, n_kv, R] fp32.
 constexpr size_t kLeanRowBytes = rows::HD * 2 + sizeof(float);
@@ -2674,12 +2698,7 @@ static int decode_attn(const char* fn, bool use_scratch, const void* q, int64_t 
     p.ws_ml = lean_lse_base(p.ws_o, size_t(2) * grid, R);
     p.two_pass = merge == PKV_DECODE_FUSED_MERGE ? 0 : 1;
     p.lean_grid = grid;
-    switch ((R + 15) / 16) {
-      case 1: decode_lean_kernel<1><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
-      case 2: decode_lean_kernel<2><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
-      case 3: decode_lean_kernel<3><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
-      default: decode_lean_kernel<4><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
-    }
+    launch_lean(p, R, batch, grid, s);
     if (p.two_pass)
       combine_lean_kernel<<<dim3(rows::NKV, batch, (R + 15) / 16), 64 * (R < 16 ? R : 16), 0, s>>>(p, grid);
     return check_launch(fn);
@@ -2832,12 +2851,7 @@ extern "C" int pkv_cascade_attn(const void* q, int64_t q_sb, int64_t q_ss, int64
   constexpr int NT = PKV_PREFILL_LDS_NT, W = PKV_PREFILL_LDS_W;
   const dim3 pgrid((batch * R + 16 * NT * W - 1) / (16 * NT * W), rows::NKV, S);
   prefill_lds_kernel<NT, W, PKV_PREFILL_LDS_NBUF, PKV_PREFILL_LDS_SUB, true><<<pgrid, 64 * W, 0, s>>>(p);
-  switch ((R + 15) / 16) {
-    case 1: decode_lean_kernel<1><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
-    case 2: decode_lean_kernel<2><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
-    case 3: decode_lean_kernel<3><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
-    default: decode_lean_kernel<4><<<grid, 64 * rows::NKV, 0, s>>>(p); break;
-  }
+  launch_lean(p, R, batch, grid, s);
   combine_lean_kernel<<<dim3(rows::NKV, batch, (R + 15) / 16), 64 * (R < 16 ? R : 16), 0, s>>>(p, grid);
   return check_launch(fn);
 }
