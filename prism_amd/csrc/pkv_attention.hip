@@ -887,7 +887,9 @@ constexpr int BUF_BYTES = 2 * TILE_BYTES + Q_BYTES;  // one LDS buffer: K tile |
 constexpr int kStreamPolicy = 2;
 // Verify (several query rows per head) reads its tiles with the default policy instead: the
 // sequences of a verify batch usually share a cached prefix, whose pages then stay in the caches
-// for the next sequence (config-5 verify: 78.3 vs 82.0 us per call).
+// for the next sequence (config-5 verify: 78.3 vs 82.0 us per call).  The suffix pass of a cascade
+// launch reads private pages only, and streams them non-temporally (config 5: 69.9 -> 65.5 us per
+// cascade call).
 constexpr int kVerifyPolicy = 0;
 typedef __attribute__((address_space(3))) void lds_void;
 }  // namespace rows
@@ -1469,13 +1471,13 @@ __device__ __forceinline__ void merge_parts_for(const AttnParams& p, int b, int 
   }
 }
 
-template <int NT, int NCH>
+template <int NT, int NCH, bool CASCADE_SUFFIX>
 __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p) {
   constexpr int HD = rows::HD;
   constexpr int DPL = HD / 16;
   constexpr bool kQInLds = NT == 1;
   constexpr int BUF = kQInLds ? rows::BUF_BYTES : 2 * rows::TILE_BYTES;
-  constexpr int kPolicy = NT == 1 ? rows::kStreamPolicy : rows::kVerifyPolicy;
+  constexpr int kPolicy = NT == 1 || CASCADE_SUFFIX ? rows::kStreamPolicy : rows::kVerifyPolicy;
   __shared__ __attribute__((aligned(16))) char lds[2 * BUF];
 
   const int lane = threadIdx.x & 63;
@@ -2418,19 +2420,20 @@ static int lean_grid(int32_t flags) {
 // decode_lean_kernel for R query rows per KV head (NT = R / 16 MFMA row tiles, rounded up) and
 // a batch of up to 64 or up to 256 sequences (the sequence table's register chunks: a kernel for
 // small batches carries a quarter of the scan and search code, which every launch fetches cold).
-template <int NT>
+template <int NT, bool CS>
 static void launch_lean_nt(const AttnParams& p, int batch, int grid, hipStream_t s) {
   if (batch <= 64)
-    decode_lean_kernel<NT, 1><<<grid, 64 * rows::NKV, 0, s>>>(p);
+    decode_lean_kernel<NT, 1, CS><<<grid, 64 * rows::NKV, 0, s>>>(p);
   else
-    decode_lean_kernel<NT, rows::kChunks><<<grid, 64 * rows::NKV, 0, s>>>(p);
+    decode_lean_kernel<NT, rows::kChunks, CS><<<grid, 64 * rows::NKV, 0, s>>>(p);
 }
 static void launch_lean(const AttnParams& p, int R, int batch, int grid, hipStream_t s) {
+  const bool cs = p.cascade_splits > 0;  // the suffix pass of a cascade launch
   switch ((R + 15) / 16) {
-    case 1: launch_lean_nt<1>(p, batch, grid, s); break;
-    case 2: launch_lean_nt<2>(p, batch, grid, s); break;
-    case 3: launch_lean_nt<3>(p, batch, grid, s); break;
-    default: launch_lean_nt<4>(p, batch, grid, s); break;
+    case 1: launch_lean_nt<1, false>(p, batch, grid, s); break;
+    case 2: cs ? launch_lean_nt<2, true>(p, batch, grid, s) : launch_lean_nt<2, false>(p, batch, grid, s); break;
+    case 3: cs ? launch_lean_nt<3, true>(p, batch, grid, s) : launch_lean_nt<3, false>(p, batch, grid, s); break;
+    default: cs ? launch_lean_nt<4, true>(p, batch, grid, s) : launch_lean_nt<4, false>(p, batch, grid, s); break;
   }
 }
 
