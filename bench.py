@@ -46,7 +46,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--workload", choices=["config2", "config3", "config4", "config5", "epilogue", "tables"], default="config3")
+    ap.add_argument("--workload", choices=["config2", "config3", "config4", "config5", "decode-14B", "decode-0.5B",
+                                           "decode-7B-tp4", "epilogue", "tables"], default="config3")
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = library choice)")
     ap.add_argument("--layers", type=int, default=0, help="layers (0 = the model's)")
     ap.add_argument("--merge", choices=["auto", "two-pass", "fused"], default="auto",
@@ -548,7 +549,10 @@ def main() -> int:
         print(json.dumps(result), flush=True)
         return 0
     print(f"[bench] building {args.workload} workload (seed={args.seed})", file=sys.stderr, flush=True)
-    w = getattr(workloads, args.workload)(dev, seed=args.seed, layers=args.layers or None)
+    if args.workload.startswith("decode-"):
+        w = workloads.ragged_decode(args.workload[len("decode-"):], dev, seed=args.seed, layers=args.layers or None)
+    else:
+        w = getattr(workloads, args.workload)(dev, seed=args.seed, layers=args.layers or None)
     L = w.layers
     outs = [torch.empty_like(q) for q in w.q]
     kv = w.kv
@@ -593,12 +597,17 @@ def main() -> int:
            "sum_ctx": int(w.ctx.sum()), "max_ctx": int(w.ctx.max()), "seed": args.seed,
            "split_tokens": args.split or "auto", "merge": args.merge}
     per_call = f"HIP events around K graph replays of the {L}-call step, per call = step / {L}"
-    if args.workload in ("config2", "config3"):
+    if args.workload in ("config2", "config3") or args.workload.startswith("decode-"):
         traffic, traffic_src = profiled_traffic(args, w)
         if args.workload == "config3":
             metric = "paged decode attn HBM GB/s (% of peak) + us/step, Qwen2.5-7B shape b=32"
             cfg["workload"] = ("config3: Qwen2.5-7B paged decode (append + attention), 28 layers, b=32, ctx "
                                "lognormal(1500, 1) in [16, 32768], 2043-page 30 GB pool, 40% churn")
+        elif args.workload.startswith("decode-"):
+            shape = w.meta["shape"]
+            metric = f"paged decode attn HBM GB/s (% of peak) + us/step, Qwen2.5-{shape} shape b={w.batch}"
+            cfg["workload"] = (f"{args.workload}: config3's ragged batch (b={w.batch}, ctx lognormal(1500, 1), 40% "
+                               f"churn) at the Qwen2.5-{shape} shape, {L} layers, {kv.max_pages}-page pool")
         else:
             metric = "paged decode attn HBM GB/s (% of peak) + us/step, Qwen2.5-7B shape b=8 ctx 2048"
             cfg["workload"] = ("config2: Qwen2.5-7B paged decode (append + attention), 28 layers, b=8, ctx 2048, "

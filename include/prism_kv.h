@@ -107,11 +107,12 @@ size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, i
  * h / (n_heads / n_kv).  Scores are scaled by softmax_scale (Prism uses the default
  * 1/sqrt(head_dim)); softmax and accumulation are fp32, out is bf16 [batch, s_q, n_heads,
  * head_dim] with the given strides.  A query row with no visible key gets zeros.
- * Two kernels serve the call.  Where head_dim = 128, n_kv = 4, page_size >= 32,
- * batch <= 256 (the Qwen2.5-7B decode and verify shapes), split_tokens = 0 and
+ * Two kernels serve the call.  Where head_dim = 128, n_kv a multiple of 4, page_size >= 32,
+ * batch <= 256 (the Qwen2.5-7B and 14B decode and verify shapes), split_tokens = 0 and
  * PKV_DECODE_HEADS is not set, a balanced kernel gives every workgroup an equal share of all
- * sequences' 32-token KV tiles; the sequences that straddle shares are merged by a second launch
- * (PKV_DECODE_FUSED_MERGE: inside the launch, by the last share of a sequence to finish).
+ * sequences' 32-token KV tiles (of every group of 4 KV heads); the sequences that straddle shares
+ * are merged by a second launch (PKV_DECODE_FUSED_MERGE: inside the launch, by the last share of a
+ * sequence to finish).
  * Otherwise a per-(sequence, KV head, split) kernel reduces split_tokens keys (a multiple of 32;
  * 0 = 512) per workgroup and merges the splits inside the launch (PKV_DECODE_TWO_PASS: in a
  * second launch).  Results agree up to rounding (fp32 order, fp16 split-K partials).

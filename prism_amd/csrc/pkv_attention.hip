@@ -58,6 +58,9 @@ struct AttnParams {
   // [k0, L) and writes every segment as a partial (whole sequences to slot 2 G + B S + b), and
   // the combine merges them all.  k0 = 0 and cascade_splits = 0 otherwise.
   int k0, cascade_splits;
+  // balanced decode kernel: the KV heads go in groups of 4 (one wave each), the tiles of group g
+  // after those of group g - 1; tok_elems = n_kv * head_dim, the elements of a token row
+  int n_groups, tok_elems;
   float scale_log2;  // softmax_scale * log2(e)
 };
 
@@ -1007,21 +1010,25 @@ __device__ __forceinline__ void locate_tile(const AttnParams& p, const SeqTable<
   }
 }
 
-// Descriptors of tiles x0 + lane (< e) of a workgroup's range: sequence, first token, lengths and
-// page.  A page id outside the pool is flagged (when the tile has keys) and kept as -1.
+// Descriptors of tiles x0 + lane (< e) of a workgroup's range: head group, sequence, first token,
+// lengths and page.  Tile x of the launch is tile x - g T1 of head group g = x / T1 (T1 tiles per
+// group).  A page id outside the pool is flagged (when the tile has keys) and kept as -1.
 struct TileWin {
   int x0;
-  int b, T0, c, L, pid;
+  int g, b, T0, c, L, pid;
 };
 
 struct TileDesc {
-  int b, T0, c, L, pid;
+  int g, b, T0, c, L, pid;
 };
 
 template <int NCH>
-__device__ __forceinline__ void tile_window(const AttnParams& p, const SeqTable<NCH>& st, int x0, int e, TileWin& w) {
+__device__ __forceinline__ void tile_window(const AttnParams& p, const SeqTable<NCH>& st, int x0, int e, int T1,
+                                            TileWin& w) {
   const int lane = threadIdx.x & 63;
-  const int x = min(x0 + lane, e - 1);
+  const int xg = min(x0 + lane, e - 1);
+  const int g = xg / T1;
+  const int x = xg - g * T1;
   int b, first, c, L;
   locate_tile(p, st, x, b, first, c, L);
   b = min(b, p.batch - 1);
@@ -1031,6 +1038,7 @@ __device__ __forceinline__ void tile_window(const AttnParams& p, const SeqTable<
   const bool ok = unsigned(pid) < unsigned(p.num_pages);
   if (!ok && T0 < L && x0 + lane < e && threadIdx.x < 64) flag_status(p.status, PKV_STATUS_BAD_PAGE);
   w.x0 = x0;
+  w.g = g;
   w.b = b;
   w.T0 = T0;
   w.c = c;
@@ -1041,6 +1049,7 @@ __device__ __forceinline__ void tile_window(const AttnParams& p, const SeqTable<
 __device__ __forceinline__ TileDesc tile_desc(const TileWin& w, int x) {
   const int i = x - w.x0;
   TileDesc d;
+  d.g = __builtin_amdgcn_readlane(w.g, i);
   d.b = __builtin_amdgcn_readlane(w.b, i);
   d.T0 = __builtin_amdgcn_readlane(w.T0, i);
   d.c = __builtin_amdgcn_readlane(w.c, i);
@@ -1054,20 +1063,21 @@ __device__ __forceinline__ bool tile_has_new(const AttnParams& p, const TileDesc
 }
 
 // Per-lane byte offsets of a wave's row copies inside a tile's K (or V) rows: copy i of wave w is
-// token row r = 4 i + w, lane l reading global chunk l ^ swz(r) of the row into LDS chunk l.  The
-// same for every tile, so they are computed once per launch.
+// token row r = 4 i + w (tok_elems * 2 bytes apart in the cache), lane l reading chunk l ^ swz(r)
+// of the row's 1 KiB head-group slice into LDS chunk l.  The same for every tile, so they are
+// computed once per launch.
 struct RowOffsets {
   uint32_t v[rows::TILE / rows::NKV];
 };
 
-__device__ __forceinline__ RowOffsets row_offsets() {
+__device__ __forceinline__ RowOffsets row_offsets(const AttnParams& p) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   RowOffsets ro;
 #pragma unroll
   for (int i = 0; i < rows::TILE / rows::NKV; ++i) {
     const int r = i * rows::NKV + wave;
-    ro.v[i] = uint32_t(r * rows::ROW_BYTES + ((lane ^ rows::swz(r)) << 4));
+    ro.v[i] = uint32_t(r * p.tok_elems * 2 + ((lane ^ rows::swz(r)) << 4));
   }
   return ro;
 }
@@ -1087,12 +1097,12 @@ __device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int64_t off = int64_t(d.pid < 0 ? 0 : d.pid) * p.page_stride +
-                      int64_t(d.T0 & ((1 << p.log2_page) - 1)) * (rows::NKV * rows::HD);
+                      int64_t(d.T0 & ((1 << p.log2_page) - 1)) * p.tok_elems + d.g * (rows::NKV * rows::HD);
+  const int tok_bytes = p.tok_elems * 2;
   if (__builtin_expect(!tile_has_new(p, d), 1)) {
-    const __amdgpu_buffer_rsrc_t rk =
-        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(p.k_cache + off), 0, rows::TILE_BYTES, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rv =
-        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(p.v_cache + off), 0, rows::TILE_BYTES, 0x00020000);
+    const int range = rows::TILE * tok_bytes;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(p.k_cache + off), 0, range, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(p.v_cache + off), 0, range, 0x00020000);
 #pragma unroll
     for (int i = I0; i < I1; ++i) {
       char* dst = buf + (i * rows::NKV + wave) * rows::ROW_BYTES;
@@ -1108,11 +1118,11 @@ __device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& 
       const int r = i * rows::NKV + wave;
       const int t = d.T0 + r;
       const uint32_t gc = uint32_t(lane ^ rows::swz(r));
-      const char* ks = kg + (r * rows::ROW_BYTES + (gc << 4));
-      const char* vs = vg + (r * rows::ROW_BYTES + (gc << 4));
+      const char* ks = kg + (r * tok_bytes + (gc << 4));
+      const char* vs = vg + (r * tok_bytes + (gc << 4));
       if (t >= d.c && t < d.L) {
         const int jn = t - d.c;
-        const int hh = int(gc >> 4);
+        const int hh = d.g * rows::NKV + int(gc >> 4);
         const int w8 = int(gc & 15) * 8;
         ks = reinterpret_cast<const char*>(p.k_new + d.b * p.kn_sb + jn * p.kn_ss + hh * p.kn_sh + w8);
         vs = reinterpret_cast<const char*>(p.v_new + d.b * p.vn_sb + jn * p.vn_ss + hh * p.vn_sh + w8);
@@ -1130,7 +1140,7 @@ __device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& 
       const int jq = rr / p.g;
       const int hq = rr - jq * p.g;
       const int gq = (lane & 15) ^ (row & 15);
-      const uint16_t* src = p.q + d.b * p.q_sb + jq * p.q_ss + (wave * p.g + hq) * p.q_sh + gq * 8;
+      const uint16_t* src = p.q + d.b * p.q_sb + jq * p.q_ss + ((d.g * rows::NKV + wave) * p.g + hq) * p.q_sh + gq * 8;
       __builtin_amdgcn_global_load_lds(src, (rows::lds_void*)(buf + 2 * rows::TILE_BYTES + (wave * 16 + 4 * i) * 256),
                                        16, 0, 0);
     }
@@ -1195,8 +1205,8 @@ __device__ __forceinline__ void rows_append_from_lds(const AttnParams& p, const 
       const int pos = (h * 16 + (li ^ rows::swz(r))) * 16;
       const u32x4 kv = *reinterpret_cast<const u32x4*>(buf + r * rows::ROW_BYTES + pos);
       const u32x4 vv = *reinterpret_cast<const u32x4*>(buf + rows::TILE_BYTES + r * rows::ROW_BYTES + pos);
-      const int64_t dst = int64_t(d.pid) * p.page_stride +
-                          int64_t(t & ((1 << p.log2_page) - 1)) * (rows::NKV * rows::HD) + h * rows::HD + 8 * li;
+      const int64_t dst = int64_t(d.pid) * p.page_stride + int64_t(t & ((1 << p.log2_page) - 1)) * p.tok_elems +
+                          (d.g * rows::NKV + h) * rows::HD + 8 * li;
       st16(p.k_cache + dst, kv);
       st16(p.v_cache + dst, vv);
     }
@@ -1273,7 +1283,7 @@ struct SeqParts {
 };
 
 template <int NCH>
-__device__ __forceinline__ SeqParts seq_parts(const AttnParams& p, const SeqTable<NCH>& st, int b, int per) {
+__device__ __forceinline__ SeqParts seq_parts(const AttnParams& p, const SeqTable<NCH>& st, int b, int base, int per) {
   int first = 0, L = 0;
 #pragma unroll
   for (int q = 0; q < NCH; ++q) {
@@ -1282,6 +1292,7 @@ __device__ __forceinline__ SeqParts seq_parts(const AttnParams& p, const SeqTabl
       L = __builtin_amdgcn_readlane(st.L[q], b & 63);
     }
   }
+  first += base;  // the group's first tile
   SeqParts sp;
   sp.w0 = first / per;
   sp.np = (first + seq_tiles(p, L) - 1) / per - sp.w0 + 1;
@@ -1326,8 +1337,8 @@ __device__ __forceinline__ void unpack_f16x8(const u32x4 v, float (&f)[8]) {
 //      lane at most: beyond ~24 the latency of such loads rises tenfold).
 // No loop body reads LDS in a dependent chain: a lane's weights come four at a time.
 template <int NC>
-__device__ __forceinline__ void merge_parts(const AttnParams& p, int b, int h, const SeqParts& sp, float* area,
-                                            int area_floats) {
+__device__ __forceinline__ void merge_parts(const AttnParams& p, int b, int h, int hout, const SeqParts& sp,
+                                            float* area, int area_floats) {
   constexpr int HD = rows::HD;
   constexpr int PB = NC >= 8 ? 1 : 8 / NC;
   const int lane = threadIdx.x & 63;
@@ -1450,24 +1461,24 @@ __device__ __forceinline__ void merge_parts(const AttnParams& p, int b, int h, c
       u32x4 ov;
 #pragma unroll
       for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[c][2 * k] * inv, acc[c][2 * k + 1] * inv);
-      st16(p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + 8 * (i & 15), ov);
+      st16(p.out + b * p.o_sb + j * p.o_ss + (hout * p.g + hq) * p.o_sh + 8 * (i & 15), ov);
     }
   }
 }
 
 // merge_parts for the row count of the launch (chunks per lane: R * 16 / 64, rounded up).
 template <int NT>
-__device__ __forceinline__ void merge_parts_for(const AttnParams& p, int b, int h, const SeqParts& sp, float* area,
-                                                int area_floats) {
+__device__ __forceinline__ void merge_parts_for(const AttnParams& p, int b, int h, int hout, const SeqParts& sp,
+                                                float* area, int area_floats) {
   if constexpr (NT == 1) {
     if (p.R <= 4)
-      merge_parts<1>(p, b, h, sp, area, area_floats);
+      merge_parts<1>(p, b, h, hout, sp, area, area_floats);
     else if (p.R <= 8)
-      merge_parts<2>(p, b, h, sp, area, area_floats);
+      merge_parts<2>(p, b, h, hout, sp, area, area_floats);
     else
-      merge_parts<4>(p, b, h, sp, area, area_floats);
+      merge_parts<4>(p, b, h, hout, sp, area, area_floats);
   } else {
-    merge_parts<4 * NT>(p, b, h, sp, area, area_floats);
+    merge_parts<4 * NT>(p, b, h, hout, sp, area, area_floats);
   }
 }
 
@@ -1487,17 +1498,19 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
 
   SeqTable<NCH> st;
   seq_table(p, st);
-  const int per = (st.total + int(gridDim.x) - 1) / int(gridDim.x);
-  const int s = min(int(blockIdx.x) * per, st.total);
-  const int e = min(s + per, st.total);
+  const int T1 = st.total;  // tiles of one head group
+  const int total = T1 * p.n_groups;
+  const int per = (total + int(gridDim.x) - 1) / int(gridDim.x);
+  const int s = min(int(blockIdx.x) * per, total);
+  const int e = min(s + per, total);
   if (s >= e) return;
   const int n = e - s;
 
   TileWin win;
-  tile_window(p, st, s, e, win);
+  tile_window(p, st, s, e, T1, win);
   TileDesc dA = tile_desc(win, s);
   TileDesc dB = dA;
-  const RowOffsets ro = row_offsets();
+  const RowOffsets ro = row_offsets(p);
   rows_issue<kPolicy>(p, dA, kQInLds, lds, ro);
   if (n > 1) {
     dB = tile_desc(win, s + 1);
@@ -1520,7 +1533,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   int seg_j0 = 0;  // range index of the current segment's first tile
   int seg_T0 = 0;  // its first token
   int stores_prev = 0, stores_prev2 = 0;  // epilogue stores of iterations j-1 and j-2 (lower bounds)
-  int pub_first = -1, pub_last = -1;  // sequences of the partials in slots 2w and 2w + 1
+  int pub_first = -1, pub_last = -1;  // segments (g * batch + b) of the partials in slots 2w, 2w + 1
   for (int j = 0; j < n; ++j) {
     const TileDesc d = dA;
     char* buf = lds + (j & 1) * BUF;
@@ -1540,7 +1553,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
       if constexpr (kQInLds)
         rows_read_q(p, buf, h, qf);
       else
-        rows_load_q<NT>(p, d, h, qf);
+        rows_load_q<NT>(p, d, d.g * rows::NKV + h, qf);
       seg_j0 = j;
       seg_T0 = d.T0;
       lim_min = 0x7fffffff;
@@ -1576,7 +1589,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     const bool next2 = j + 2 < n;
     if (next2) {
       const int x2 = s + j + 2;
-      if (x2 - win.x0 >= 64) tile_window(p, st, x2, e, win);
+      if (x2 - win.x0 >= 64) tile_window(p, st, x2, e, T1, win);
       d2 = tile_desc(win, x2);
       rows_issue<kPolicy>(p, d2, false, buf, ro, 0, 4);
     }
@@ -1614,7 +1627,8 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
           const int jr = rr / p.g;
           const int hq = rr - jr * p.g;
           const float inv = lsum[nt] > 0.f ? 1.f / lsum[nt] : 0.f;
-          uint16_t* dst = p.out + d.b * p.o_sb + jr * p.o_ss + (h * p.g + hq) * p.o_sh + 4 * DPL * lq;
+          uint16_t* dst =
+              p.out + d.b * p.o_sb + jr * p.o_ss + ((d.g * rows::NKV + h) * p.g + hq) * p.o_sh + 4 * DPL * lq;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             u32x4 ov;
@@ -1630,12 +1644,13 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
       // or by the combine launch (two-pass)
       const int slot = complete ? 2 * p.lean_grid + p.batch * p.cascade_splits + d.b
                                 : 2 * int(blockIdx.x) + (seg_j0 == 0 ? 0 : 1);
+      // the merge below names a segment by g * batch + b
       if (complete)
         ;
       else if (seg_j0 == 0)
-        pub_first = d.b;
+        pub_first = d.g * p.batch + d.b;
       else
-        pub_last = d.b;
+        pub_last = d.g * p.batch + d.b;
       const uint32_t lse0 = uint32_t(p.ws_ml - p.ws_o) * 4u;
       const __amdgpu_buffer_rsrc_t rs = ws_rsrc(p);
       bool ovf = false;
@@ -1686,12 +1701,14 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   prev1 = __builtin_amdgcn_readfirstlane(prev1);
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
-    const int b = k == 0 ? pub_first : pub_last;
-    if (b < 0) continue;
-    const SeqParts sp = seq_parts(p, st, b, per);
+    const int seg = k == 0 ? pub_first : pub_last;
+    if (seg < 0) continue;
+    const int g = seg / p.batch;
+    const int b = seg - g * p.batch;
+    const SeqParts sp = seq_parts(p, st, b, g * T1, per);
     if ((k == 0 ? prev0 : prev1) != sp.np - 1) continue;
-    if (lane == 0) __hip_atomic_store(p.ws_cnt + b * rows::NKV + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_parts_for<NT>(p, b, h, sp, area, 2 * BUF / rows::NKV / 4);
+    if (lane == 0) __hip_atomic_store(p.ws_cnt + seg * rows::NKV + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    merge_parts_for<NT>(p, b, h, g * rows::NKV + h, sp, area, 2 * BUF / rows::NKV / 4);
   }
 }
 
@@ -1727,7 +1744,9 @@ constexpr int kLeanMergeParts = 64;
 __global__ __launch_bounds__(1024) void combine_lean_kernel(const AttnParams p, int grid) {
   constexpr int HD = rows::HD;
   static_assert(HD == 128, "16 lanes x 16 bytes per part row");
-  const int h = blockIdx.x;
+  const int hg = blockIdx.x;  // KV head; its group's tiles follow those of the groups before it
+  const int g = hg / rows::NKV;
+  const int h = hg - g * rows::NKV;  // head within the group (the partials hold 4 per slot)
   const int b = blockIdx.y;
   const int r = int(blockIdx.z) * 16 + int(threadIdx.x >> 6);  // query row of this wave
   const int lane = threadIdx.x & 63;
@@ -1755,7 +1774,8 @@ __global__ __launch_bounds__(1024) void combine_lean_kernel(const AttnParams p, 
     }
     total = __builtin_amdgcn_readlane(incl, 63);
   }
-  const int per = (total + grid - 1) / grid;
+  const int per = (total * p.n_groups + grid - 1) / grid;
+  first += g * total;
   const int w0 = first / per;
   const int np = (first + seq_tiles(p, L) - 1) / per - w0 + 1;
   // cascade: the prefix pass's S parts first, then the sequence's suffix partial(s)
@@ -1825,7 +1845,7 @@ __global__ __launch_bounds__(1024) void combine_lean_kernel(const AttnParams p, 
     u32x4 ov;
 #pragma unroll
     for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[2 * k] * inv, acc[2 * k + 1] * inv);
-    st16(p.out + b * p.o_sb + j * p.o_ss + (h * p.g + hq) * p.o_sh + 8 * dc, ov);
+    st16(p.out + b * p.o_sb + j * p.o_ss + (hg * p.g + hq) * p.o_sh + 8 * dc, ov);
   }
 }
 
@@ -2407,8 +2427,9 @@ static size_t ws_bytes(int batch, int R, int n_kv, int head_dim, int64_t max_spl
 constexpr int kLeanMaxRows = PKV_LEAN_MAX_ROWS;
 static bool use_lean_kernel(int batch, int head_dim, int n_kv, int R, int page_size, int split_tokens,
                             int32_t flags) {
-  return head_dim == rows::HD && n_kv == rows::NKV && R <= kLeanMaxRows && page_size >= rows::TILE &&
-         batch <= rows::kMaxBatch && split_tokens <= 0 && !(flags & PKV_DECODE_HEADS);
+  return head_dim == rows::HD && n_kv % rows::NKV == 0 && R <= kLeanMaxRows && page_size >= rows::TILE &&
+         batch <= rows::kMaxBatch && int64_t(batch) * n_kv <= kMaxCounters && split_tokens <= 0 &&
+         !(flags & PKV_DECODE_HEADS);
 }
 
 // Workgroups of a decode_lean_kernel launch: PKV_DECODE_GRID(n) of the flags, else one per CU.
@@ -2514,6 +2535,8 @@ static void fill_params(AttnParams& p, const void* q, int64_t q_sb, int64_t q_ss
   p.lean_grid = 0;
   p.k0 = 0;
   p.cascade_splits = 0;
+  p.n_groups = 1;
+  p.tok_elems = 0;  // set by the balanced-kernel launches
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
 }
 
@@ -2701,9 +2724,11 @@ static int decode_attn(const char* fn, bool use_scratch, const void* q, int64_t 
     p.ws_ml = lean_lse_base(p.ws_o, size_t(2) * grid, R);
     p.two_pass = merge == PKV_DECODE_FUSED_MERGE ? 0 : 1;
     p.lean_grid = grid;
+    p.n_groups = n_kv / rows::NKV;
+    p.tok_elems = n_kv * head_dim;
     launch_lean(p, R, batch, grid, s);
     if (p.two_pass)
-      combine_lean_kernel<<<dim3(rows::NKV, batch, (R + 15) / 16), 64 * (R < 16 ? R : 16), 0, s>>>(p, grid);
+      combine_lean_kernel<<<dim3(n_kv, batch, (R + 15) / 16), 64 * (R < 16 ? R : 16), 0, s>>>(p, grid);
     return check_launch(fn);
   }
 
@@ -2768,7 +2793,7 @@ namespace pkv {
 
 static bool cascade_eligible(int batch, int head_dim, int n_kv, int R, int page_size, int max_blocks,
                              int shared_tokens) {
-  return use_lean_kernel(batch, head_dim, n_kv, R, page_size, 0, 0) && shared_tokens > 0 &&
+  return n_kv == rows::NKV && use_lean_kernel(batch, head_dim, n_kv, R, page_size, 0, 0) && shared_tokens > 0 &&
          shared_tokens % page_size == 0 && int64_t(shared_tokens) <= int64_t(max_blocks) * page_size;
 }
 
@@ -2848,6 +2873,7 @@ extern "C" int pkv_cascade_attn(const void* q, int64_t q_sb, int64_t q_ss, int64
   p.ws_ml = lean_lse_base(p.ws_o, slots, R);
   p.two_pass = 1;
   p.lean_grid = grid;
+  p.tok_elems = n_kv * head_dim;
   p.k0 = shared_tokens;
   p.cascade_splits = S;
   hipStream_t s = static_cast<hipStream_t>(stream);

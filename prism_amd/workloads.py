@@ -24,6 +24,8 @@ SHAPES = {
     "0.5B": dict(n_heads=14, n_kv=2, head_dim=64, layers=24),
     "7B": dict(n_heads=28, n_kv=4, head_dim=128, layers=28),
     "14B": dict(n_heads=40, n_kv=8, head_dim=128, layers=48),
+    # one GPU's share of the 7B model under 4-way tensor parallelism (KV heads split across GPUs)
+    "7B-tp4": dict(n_heads=7, n_kv=1, head_dim=128, layers=28),
 }
 PAGE = 256
 
@@ -168,6 +170,30 @@ def config3(device="cuda", seed=0, layers=None, max_pages=None, batch=32, churn=
     _alloc(kv, range(batch), ctx, 1)
     return _finish("config3", kv, list(range(batch)), ctx, 1, s["n_heads"], g, device,
                    {"shape": "7B", "pool_pages": mp, "free_after_churn": len(freed)})
+
+
+def ragged_decode(shape: str, device="cuda", seed=0, layers=None, max_pages=None, batch=32, churn=0.4,
+                  budget_gb=30.0) -> PagedWorkload:
+    """config3's ragged decode batch (lognormal lengths, churned pool, LIFO allocation) at another
+    model shape: the Qwen2.5-14B (8 KV heads) and 0.5B (2 KV heads, head_dim 64) decode steps, and
+    the 7B step on one GPU of a 4-way tensor-parallel group (1 KV head).  The pool is the model's
+    30 GB budget, capped at 4096 pages."""
+    s = SHAPES[shape]
+    L = layers or s["layers"]
+    rng = np.random.default_rng(seed)
+    mp = max_pages or min(pages_for_budget(budget_gb, s["layers"], s["n_kv"], s["head_dim"]), 4096)
+    kv = FlashAttnKVCache(L, s["n_kv"], s["head_dim"], mp, PAGE, device, torch.bfloat16)
+    g = _gen(device, seed)
+    _fill_pool(kv, g)
+    ctx = lognormal_ctx(rng, batch)
+    freed = rng.permutation(mp)[: int(round(churn * mp))]
+    need = int(np.ceil((ctx + 1) / PAGE).sum())
+    if need > len(freed):
+        raise RuntimeError(f"ragged_decode {shape} seed {seed}: {need} pages needed > {len(freed)} free")
+    kv.free_pages = [int(p) for p in freed]
+    _alloc(kv, range(batch), ctx, 1)
+    return _finish(f"decode-{shape}", kv, list(range(batch)), ctx, 1, s["n_heads"], g, device,
+                   {"shape": shape, "pool_pages": mp})
 
 
 def config4(device="cuda", seed=0, layers=None, max_pages=None, batch=8, chunk=512, max_prefix=4096) -> PagedWorkload:

@@ -116,6 +116,27 @@ def test_balanced_decode_kernel(gpu, case, merge):
                    what=f"lean{case[:1] + case[2:]}-{merge}")
 
 
+# The balanced kernel with KV heads in groups of four (8 and 12 KV heads: Qwen2.5-14B, and a
+# larger GQA model), decode and verify row counts, both merges: a range may straddle two head groups.
+GROUP_CASES = [
+    # (batch, ctx, page, n_kv, n_heads, s_q, grid)
+    (6, [3000, 17, 4100, 800, 1, 2500], 256, 8, 40, 1, 0),
+    (6, [3000, 17, 4100, 800, 1, 2500], 256, 8, 40, 1, 7),
+    (3, [517, 2, 90], 256, 8, 40, 5, 0),                      # R = 25: two row tiles
+    (40, [(i * 37) % 300 for i in range(40)], 32, 8, 40, 1, 5),
+    (5, [10, 2000, 30, 40, 50], 64, 12, 48, 2, 3),           # three head groups, R = 8
+    (1, [0], 256, 8, 64, 1, 1),                               # empty cache, g = 8
+]
+
+
+@pytest.mark.parametrize("merge", ["two-pass", "in-launch"])
+@pytest.mark.parametrize("case", GROUP_CASES, ids=[f"g{i}" for i in range(len(GROUP_CASES))])
+def test_balanced_kernel_head_groups(gpu, case, merge):
+    B, ctx, P, n_kv, nh, s_q, grid = case
+    _run_and_check(gpu, batch=B, ctx=ctx, page_size=P, n_kv=n_kv, n_heads=nh, head_dim=128, s_q=s_q,
+                   grid=grid, two_pass=merge == "two-pass", seed=len(ctx) + grid, what=f"groups{case}-{merge}")
+
+
 def test_balanced_in_launch_merge_rearms_across_calls(gpu):
     # the balanced kernel's per-(sequence, head) arrival counters must be back at zero after every
     # call: consecutive calls of different shapes and grids share one workspace, with sequences

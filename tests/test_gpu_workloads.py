@@ -173,6 +173,17 @@ def test_config2_decode(gpu):
     _free()
 
 
+@pytest.mark.parametrize("shape", ["14B", "0.5B", "7B-tp4"])
+def test_ragged_decode_other_shapes(gpu, shape):
+    # config 3's ragged batch at the 14B (8 KV heads), 0.5B (2 KV heads, head_dim 64) and 7B
+    # tensor-parallel-shard (1 KV head) shapes, first and last layer
+    w = workloads.ragged_decode(shape, gpu, seed=0)
+    assert int(w.ctx.sum()) == 55816
+    _decode_layers(w, [0, w.layers - 1], f"decode-{shape}")
+    del w
+    _free()
+
+
 def test_config4_chunked_prefill(gpu):
     # 14B: 8 chunks of 512 appended onto prefixes ~U{0..4096}, causal within the chunk; the fp64
     # oracle on KV heads 0 and 5 (query heads 0-4 and 25-29) of every sequence and row
