@@ -21,6 +21,9 @@ epilogue times the elementwise kernels on either side of attention (QKV split + 
 append, RMSNorm with the residual add, SiLU-mul) at the 14B prefill-chunk and 7B decode scales.
 --workload tables times the per-step host staging of a graph-captured decode batch (block table,
 lengths, rotary rows) at config 3's batch: DecodeBatch against the reference's refill.
+--workload decode-14B / decode-0.5B / decode-7B-tp4 run config 3's ragged batch at other model
+shapes.  --workload peak measures the streaming-read ceiling of the decode kernels' copy pattern
+(libpkv_probe.so) that the roofline's published 8 TB/s is checked against.
 """
 from __future__ import annotations
 
@@ -47,7 +50,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--workload", choices=["config2", "config3", "config4", "config5", "decode-14B", "decode-0.5B",
-                                           "decode-7B-tp4", "epilogue", "tables"], default="config3")
+                                           "decode-7B-tp4", "epilogue", "tables", "peak"], default="config3")
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = library choice)")
     ap.add_argument("--layers", type=int, default=0, help="layers (0 = the model's)")
     ap.add_argument("--merge", choices=["auto", "two-pass", "fused"], default="auto",
@@ -479,6 +482,52 @@ def tables_bench(args, dev) -> dict:
             "max_pages_per_seq": max(len(kv.seq_pages[b]) for b in ids)}
 
 
+def peak_bench(args, dev) -> dict:
+    """Streaming-read rates of the decode kernels' copy pattern (global->LDS, 1 KiB per wave
+    instruction, one 4-wave workgroup per CU) from a buffer far larger than the caches, read once
+    (HBM), and from a 64 MiB window re-read by every workgroup (last-level cache): the measured
+    ceiling that the HBM roofline's published 8 TB/s is checked against."""
+    import ctypes
+
+    import torch
+
+    from prism_amd.build import PROBE_LIB_PATH
+
+    if not PROBE_LIB_PATH.exists():
+        raise RuntimeError(f"{PROBE_LIB_PATH} is not built: run __graft_entry__.build() first")
+    lib = ctypes.CDLL(str(PROBE_LIB_PATH))
+    lib.pkv_probe_stream_read.restype = ctypes.c_int
+    lib.pkv_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int,
+                                          ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    grid = torch.cuda.get_device_properties(dev).multi_processor_count
+    per_wg = 32 << 20  # 32 MiB per workgroup: 8 GiB over 256 CUs
+    buf = torch.randint(0, 255, (grid * per_wg,), dtype=torch.uint8, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    for name, window, policy in (("hbm_nt", grid * per_wg, 2), ("hbm_default", grid * per_wg, 0),
+                                 ("llc_64mib", 64 << 20, 0)):
+        def launch():
+            rc = lib.pkv_probe_stream_read(buf.data_ptr(), window, per_wg, grid, policy, sink.data_ptr(),
+                                           stream.cuda_stream)
+            if rc:
+                raise RuntimeError(f"pkv_probe_stream_read returned {rc}")
+
+        for _ in range(2):
+            launch()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            launch()
+        e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / args.steps
+        res[name] = {"bytes": grid * per_wg, "us": round(us, 1), "gbs": round(grid * per_wg / (us * 1e-6) / 1e9, 1)}
+        print(f"[bench] peak {name}: {res[name]}", file=sys.stderr, flush=True)
+    del buf
+    return res
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -517,6 +566,25 @@ def main() -> int:
         }
         if not args.no_cpu_baseline:
             result["cpu_baseline"] = epilogue_cpu_baseline(args.seed)
+        print(json.dumps(result), flush=True)
+        return 0
+    if args.workload == "peak":
+        res = peak_bench(args, dev)
+        best = max(res["hbm_nt"]["gbs"], res["hbm_default"]["gbs"])
+        result = {
+            "metric": "streaming HBM read GB/s of the decode kernels' global->LDS copy pattern (8 GiB, read once)",
+            "value": best, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": 2,
+            "ms_per_step": round(res["hbm_nt"]["us"] / 1e3, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "u8", "data": "synthetic",
+            "config": {"workload": "peak: one 4-wave workgroup per CU streams 32 MiB of an 8 GiB buffer into LDS "
+                                   "(1 KiB per wave copy, 32 KiB stages, two in flight), non-temporal and default "
+                                   "cache policy, then a 64 MiB window every workgroup re-reads"},
+            "roofline": {"bound": "hbm", "achieved": best, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(best / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "stream_read_kernel (libpkv_probe.so); HIP events around K launches",
+                         "bytes_per_call": res["hbm_nt"]["bytes"], "avg_call_us": res["hbm_nt"]["us"]},
+            "detail": res,
+        }
         print(json.dumps(result), flush=True)
         return 0
     if args.workload == "tables":

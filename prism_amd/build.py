@@ -19,6 +19,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libprism_kv.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+PROBE_LIB_PATH = PKG_DIR / "libpkv_probe.so"
 BUILD_DIR = PKG_DIR / "_build"
 ARCH = "gfx950"
 
@@ -85,6 +86,13 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH}")
+    # the bandwidth probe bench.py --workload peak runs: its own library, outside the paged-KV ABI
+    probe_src = PKG_DIR / "csrc_probe" / "pkv_probe.hip"
+    probe_tmp = PROBE_LIB_PATH.with_suffix(".so.tmp")
+    _run([hipcc, *HIPCC_FLAGS, *extra, "-shared", "-o", str(probe_tmp), str(probe_src)])
+    os.replace(probe_tmp, PROBE_LIB_PATH)
+    if verbose:
+        print(f"built {PROBE_LIB_PATH}")
     return LIB_PATH
 
 
