@@ -57,10 +57,15 @@ extern "C" {
 #define PKV_STATUS_PARTIAL_RANGE 8 /* a balanced-kernel split-K partial (fp16 O / l) would exceed
                                       fp16's range: |V| >= 65520 somewhere; that output is inf.
                                       PKV_DECODE_HEADS keeps fp32 partials */
+#define PKV_STATUS_MERGE_TIMEOUT 16 /* an in-launch merge (PKV_DECODE_FUSED_MERGE) waited past its
+                                       bound for a sequence's split-K parts; that output is stale.
+                                       Never expected: it reports a broken arrival count */
 
 /* pkv_decode_attn flags (0 = the library's choice of kernel and merge) */
 #define PKV_DECODE_TWO_PASS 1    /* merge split-K partials in a second launch */
-#define PKV_DECODE_FUSED_MERGE 2 /* merge split-K partials in the attention launch (last part to finish) */
+#define PKV_DECODE_FUSED_MERGE 2 /* merge split-K partials in the attention launch (per-head kernel:
+                                    the last split to finish; balanced kernel with <= 16 query rows
+                                    per KV head: merge workgroups appended to its grid) */
 #define PKV_DECODE_HEADS 4       /* use the per-head kernel where the balanced one would run */
 #define PKV_DECODE_GRID(n) ((int32_t)(n) << 8) /* balanced kernel on n (1..65535) workgroups, not one per CU */
 
@@ -107,12 +112,14 @@ size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, i
  * h / (n_heads / n_kv).  Scores are scaled by softmax_scale (Prism uses the default
  * 1/sqrt(head_dim)); softmax and accumulation are fp32, out is bf16 [batch, s_q, n_heads,
  * head_dim] with the given strides.  A query row with no visible key gets zeros.
- * Two kernels serve the call.  Where head_dim = 128, n_kv a multiple of 4, page_size >= 32,
- * batch <= 256 (the Qwen2.5-7B and 14B decode and verify shapes), split_tokens = 0 and
- * PKV_DECODE_HEADS is not set, a balanced kernel gives every workgroup an equal share of all
- * sequences' 32-token KV tiles (of every group of 4 KV heads); the sequences that straddle shares
- * are merged by a second launch (PKV_DECODE_FUSED_MERGE: inside the launch, by the last share of a
- * sequence to finish).
+ * Two kernels serve the call.  Where head_dim = 128 (any n_kv) or head_dim = 64 with an even
+ * n_kv (the Qwen2.5 decode and verify shapes, 0.5B to 72B, and their tensor-parallel shards),
+ * batch <= 256, split_tokens = 0 and PKV_DECODE_HEADS is not set, a balanced kernel gives every
+ * workgroup an equal share of all sequences' KV tiles (of every group of 4, 2 or 1 KV heads; a
+ * tile is 32 tokens of 4 heads x 128, 64 of 2 x 128 or 4 x 64, 128 of 1 x 128 or 2 x 64, and
+ * page_size must hold a whole tile); the sequences that straddle shares are merged by a second
+ * launch (PKV_DECODE_FUSED_MERGE, for decode's <= 16 query rows per KV head: inside the launch,
+ * by merge workgroups that wait for a sequence's shares; measured on par with the second launch).
  * Otherwise a per-(sequence, KV head, split) kernel reduces split_tokens keys (a multiple of 32;
  * 0 = 512) per workgroup and merges the splits inside the launch (PKV_DECODE_TWO_PASS: in a
  * second launch).  Results agree up to rounding (fp32 order, fp16 split-K partials).

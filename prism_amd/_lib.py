@@ -22,6 +22,7 @@ PKV_STATUS_BAD_PAGE = 1
 PKV_STATUS_BAD_POSITION = 2
 PKV_STATUS_SHARED_PREFIX = 4
 PKV_STATUS_PARTIAL_RANGE = 8
+PKV_STATUS_MERGE_TIMEOUT = 16
 PKV_DECODE_TWO_PASS = 1
 PKV_DECODE_FUSED_MERGE = 2
 PKV_DECODE_HEADS = 4

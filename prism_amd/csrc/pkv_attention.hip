@@ -58,9 +58,10 @@ struct AttnParams {
   // [k0, L) and writes every segment as a partial (whole sequences to slot 2 G + B S + b), and
   // the combine merges them all.  k0 = 0 and cascade_splits = 0 otherwise.
   int k0, cascade_splits;
-  // balanced decode kernel: the KV heads go in groups of 4 (one wave each), the tiles of group g
-  // after those of group g - 1; tok_elems = n_kv * head_dim, the elements of a token row
-  int n_groups, tok_elems;
+  // balanced decode kernel: the KV heads go in n_groups head groups, the tiles of group g after
+  // those of group g - 1; tok_elems = n_kv * head_dim, the elements of a token row; cnt_stride:
+  // int32 words between the in-launch merge's arrival counters
+  int n_groups, tok_elems, cnt_stride;
   float scale_log2;  // softmax_scale * log2(e)
 };
 
@@ -873,17 +874,17 @@ __global__ __launch_bounds__(512) void combine_kernel(const AttnParams p) {
 // rows during the launch, so nothing orders the append before the attention reads.
 // ---------------------------------------------------------------------------------------------
 namespace rows {
-// chunk swizzle of row r (bits 0-3 of the 16-byte chunk index; stays inside the head's 256 B)
+// chunk swizzle of row r (bits 0-3 of the 16-byte chunk index; stays inside a wave's 256 B slice)
 __device__ __forceinline__ int swz(int r) { return (r & 3) | (((r >> 3) & 3) << 2); }
+// The 4 KV heads x head_dim 128 geometry: the cascade path's, and the per-slot bound of the
+// split-K workspace (no geometry holds more than 4 x 128 elements per partial row block).
 constexpr int HD = 128;
 constexpr int NKV = 4;
-constexpr int ROW_BYTES = NKV * HD * 2;   // 1 KiB
-constexpr int TILE = 32;                  // tokens per tile
+constexpr int ROW_BYTES = 1024;           // one LDS row: four 256-byte wave slices
+constexpr int TILE = 32;                  // LDS rows per tile = keys per MFMA subtile
 constexpr int TILE_BYTES = TILE * ROW_BYTES;
 constexpr int kMaxBatch = 256;            // sequences the in-register scan covers
 constexpr int kChunks = kMaxBatch / 64;
-constexpr int Q_BYTES = 16 * NKV * HD * 2; // Q operand area: <= 16 rows x 4 heads x 256 B
-constexpr int BUF_BYTES = 2 * TILE_BYTES + Q_BYTES;  // one LDS buffer: K tile | V tile | Q
 // Cache policy of the K/V tile copies: non-temporal (the nt bit).  Every cache byte is read once
 // per call, and streaming it past the caches' normal allocation measured ~12% faster for the
 // 7B decode step's 115 MB (18.7 vs 21.1 us per launch for the bare copy loop).
@@ -896,6 +897,32 @@ constexpr int kStreamPolicy = 2;
 constexpr int kVerifyPolicy = 0;
 typedef __attribute__((address_space(3))) void lds_void;
 }  // namespace rows
+
+// Geometry of a balanced launch: HG KV heads of head_dim HD form a head group, whose slice of a
+// token row (HG * HD * 2 bytes: 1 KiB, 512 B or 256 B) the four waves share.  Wave w takes the
+// 256-byte slice w of every 1 KiB LDS row: head hg = w % HG of the group, phase ph = w / HG.  With
+// P = 4 / HG phases the LDS row packs P token rows: a tile holds TOK = 32 P S tokens and wave
+// (hg, ph) owns the consecutive keys [32 S ph, 32 S (ph + 1)) of it for head hg, as S 32-key MFMA
+// subtiles (S = 2 at head_dim 64, whose head slice is 128 B).  The P phases of a head keep
+// separate softmax states, merged through LDS when a segment ends.  Geom<128, 4> is the 7B shape
+// (one token row of four heads per LDS row, no phases).
+template <int HD_, int HG_>
+struct Geom {
+  static_assert(HD_ == 64 || HD_ == 128, "head_dim 64 or 128");
+  static_assert(HG_ == 1 || HG_ == 2 || HG_ == 4, "1, 2 or 4 KV heads per group");
+  static constexpr int HD = HD_;
+  static constexpr int HG = HG_;
+  static constexpr int S = 128 / HD;                 // 32-key subtiles per wave and tile
+  static constexpr int P = 4 / HG;                   // phases (waves per head)
+  static constexpr int TOK = rows::TILE * P * S;     // tokens per tile
+  static constexpr int SCH = 16 / S;                 // 16-byte chunks of one head row (HD / 8)
+  static constexpr int QROW = HD * 2;                // bytes of one Q row
+  static constexpr int QCH = QROW / 16;
+  static constexpr int Q_BYTES = 16 * HG * QROW;     // Q area: 16 rows per head of the group
+  static constexpr int Q_COPIES = Q_BYTES / 4096;    // 1 KiB copies per wave that fill it
+  static_assert(Q_COPIES >= 1, "the Q area must give every wave a copy");
+};
+using Geom7B = Geom<128, 4>;
 
 // Workgroup barrier that only orders memory operations for the compiler: the hardware waits for
 // nothing beyond the explicit s_waitcnt the caller issued (a __syncthreads fence would also
@@ -927,12 +954,15 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
-__device__ __forceinline__ int tiles_of(int L) { return L > 0 ? (L + rows::TILE - 1) / rows::TILE : 1; }
+template <int TOK>
+__device__ __forceinline__ int tiles_of(int L) { return L > 0 ? (L + TOK - 1) / TOK : 1; }
 
-// Tiles of a sequence of L keys in a balanced launch: keys [k0, L) (k0 tile-aligned), at least one
-// (a sequence without keys there still yields its zero output or empty partial).
+// Tiles of TOK tokens of a sequence of L keys in a balanced launch: keys [k0, L) (k0
+// tile-aligned), at least one (a sequence without keys there still yields its zero output or
+// empty partial).
+template <int TOK>
 __device__ __forceinline__ int seq_tiles(const AttnParams& p, int L) {
-  const int t = tiles_of(L) - p.k0 / rows::TILE;
+  const int t = tiles_of<TOK>(L) - p.k0 / TOK;
   return t > 0 ? t : 1;
 }
 
@@ -945,7 +975,7 @@ struct SeqTable {
   int total;               // T, tiles over all sequences
 };
 
-template <int NCH>
+template <int NCH, int TOK>
 __device__ __forceinline__ void seq_table(const AttnParams& p, SeqTable<NCH>& st) {
   const int lane = threadIdx.x & 63;
   const int cap = p.max_blocks << p.log2_page;
@@ -968,7 +998,7 @@ __device__ __forceinline__ void seq_table(const AttnParams& p, SeqTable<NCH>& st
       c = min(max(c, 0), cap);
       L = min(c + s_new, cap);
     }
-    const int n = b < p.batch ? seq_tiles(p, L) : 0;
+    const int n = b < p.batch ? seq_tiles<TOK>(p, L) : 0;
     const int incl = base + wave_incl_scan(n);
     st.c[q] = c;
     st.L[q] = L;
@@ -1022,7 +1052,7 @@ struct TileDesc {
   int g, b, T0, c, L, pid;
 };
 
-template <int NCH>
+template <int NCH, int TOK>
 __device__ __forceinline__ void tile_window(const AttnParams& p, const SeqTable<NCH>& st, int x0, int e, int T1,
                                             TileWin& w) {
   const int lane = threadIdx.x & 63;
@@ -1032,7 +1062,7 @@ __device__ __forceinline__ void tile_window(const AttnParams& p, const SeqTable<
   int b, first, c, L;
   locate_tile(p, st, x, b, first, c, L);
   b = min(b, p.batch - 1);
-  const int T0 = (x - first) * rows::TILE + p.k0;
+  const int T0 = (x - first) * TOK + p.k0;
   const int col = T0 >> p.log2_page;
   const int pid = unsigned(col) < unsigned(p.max_blocks) ? p.block_table[int64_t(b) * p.bt_stride + col] : -1;
   const bool ok = unsigned(pid) < unsigned(p.num_pages);
@@ -1058,54 +1088,76 @@ __device__ __forceinline__ TileDesc tile_desc(const TileWin& w, int x) {
   return d;
 }
 
+template <int TOK>
 __device__ __forceinline__ bool tile_has_new(const AttnParams& p, const TileDesc& d) {
-  return p.has_new && d.T0 + rows::TILE > d.c && d.T0 < d.L;
+  return p.has_new && d.T0 + TOK > d.c && d.T0 < d.L;
 }
 
-// Per-lane byte offsets of a wave's row copies inside a tile's K (or V) rows: copy i of wave w is
-// token row r = 4 i + w (tok_elems * 2 bytes apart in the cache), lane l reading chunk l ^ swz(r)
-// of the row's 1 KiB head-group slice into LDS chunk l.  The same for every tile, so they are
-// computed once per launch.
-struct RowOffsets {
-  uint32_t v[rows::TILE / rows::NKV];
+// Where lane l's 16 bytes of LDS row r of a tile come from: LDS chunk l holds chunk
+// v = (l & 15) ^ swz(r) of wave slice w = l / 16 (head hg = w % HG, phase ph = w / HG): chunk
+// v % SCH of head hg's row of token 32 (S ph + v / SCH) + r of the tile.
+template <typename G>
+struct LaneSrc {
+  int tt;  // token within the tile
+  int hg;  // head within the group
+  int cc;  // 16-byte chunk within the head row
 };
 
+template <typename G>
+__device__ __forceinline__ LaneSrc<G> lane_src(int r, int lane) {
+  const int w = lane >> 4;
+  const int v = (lane & 15) ^ rows::swz(r);
+  LaneSrc<G> ls;
+  ls.hg = w % G::HG;
+  ls.tt = rows::TILE * ((w / G::HG) * G::S + v / G::SCH) + r;
+  ls.cc = v % G::SCH;
+  return ls;
+}
+
+// Per-lane byte offsets of a wave's row copies inside a tile's K (or V) run: copy i of wave w
+// fills LDS row r = 4 i + w (lane_src gives the token, head and chunk; tok_elems * 2 bytes per
+// token).  The same for every tile, so they are computed once per launch.
+struct RowOffsets {
+  uint32_t v[rows::TILE / 4];
+};
+
+template <typename G>
 __device__ __forceinline__ RowOffsets row_offsets(const AttnParams& p) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   RowOffsets ro;
 #pragma unroll
-  for (int i = 0; i < rows::TILE / rows::NKV; ++i) {
-    const int r = i * rows::NKV + wave;
-    ro.v[i] = uint32_t(r * p.tok_elems * 2 + ((lane ^ rows::swz(r)) << 4));
+  for (int i = 0; i < rows::TILE / 4; ++i) {
+    const LaneSrc<G> ls = lane_src<G>(i * 4 + wave, lane);
+    ro.v[i] = uint32_t(ls.tt * p.tok_elems * 2 + ls.hg * G::HD * 2 + ls.cc * 16);
   }
   return ro;
 }
 
-// Copies of tile d into LDS buffer `buf`, 16 per wave: K then V rows of every head, wave w taking
-// rows w, w + 4, ..., lane l writing LDS chunk l of a row from global chunk l ^ swz(row).  A tile
-// without new rows is two buffers (its K rows and its V rows, 32 KiB each, base and range in
-// scalar registers) read at the precomputed lane offsets: one M0 write and one buffer load per
-// copy.  In a tile holding one of this call's new tokens (t >= c), that row's copy is sourced
-// from k_new / v_new instead of the cache, so attention sees it without waiting for the append.
-// When the tile starts a segment (with_q), 4 more copies per wave bring the Q operand rows of
-// head w into the buffer's Q area: row r (clamped to R - 1) at [w][r], LDS chunk l holding global
-// chunk l ^ (r & 15).
-template <int POLICY = rows::kStreamPolicy>
+// Copies of tile d into LDS buffer `buf`, 16 per wave: K then V rows, wave w filling LDS rows
+// w, w + 4, ..., lane l writing LDS chunk l of a row (row_offsets' mapping).  A tile without new
+// rows is two buffers (its K and its V run, TOK token rows each, base and range in scalar
+// registers) read at the precomputed lane offsets: one M0 write and one buffer load per copy.
+// In a tile holding one of this call's new tokens (t >= c), that token's chunks are sourced from
+// k_new / v_new instead of the cache, so attention sees them without waiting for the append.
+// When the tile starts a segment (with_q), Q_COPIES more copies per wave bring the Q operand rows
+// of the group's heads into the buffer's Q area: row r (clamped to R - 1) of head hg at
+// [hg][r], LDS chunk c holding global chunk c ^ (r % QCH).
+template <typename G, int POLICY = rows::kStreamPolicy>
 __device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& d, bool with_q, char* buf,
-                                           const RowOffsets& ro, int I0 = 0, int I1 = rows::TILE / rows::NKV) {
+                                           const RowOffsets& ro, int I0 = 0, int I1 = rows::TILE / 4) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int64_t off = int64_t(d.pid < 0 ? 0 : d.pid) * p.page_stride +
-                      int64_t(d.T0 & ((1 << p.log2_page) - 1)) * p.tok_elems + d.g * (rows::NKV * rows::HD);
+                      int64_t(d.T0 & ((1 << p.log2_page) - 1)) * p.tok_elems + d.g * (G::HG * G::HD);
   const int tok_bytes = p.tok_elems * 2;
-  if (__builtin_expect(!tile_has_new(p, d), 1)) {
-    const int range = rows::TILE * tok_bytes;
+  if (__builtin_expect(!tile_has_new<G::TOK>(p, d), 1)) {
+    const int range = G::TOK * tok_bytes;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(p.k_cache + off), 0, range, 0x00020000);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(p.v_cache + off), 0, range, 0x00020000);
 #pragma unroll
     for (int i = I0; i < I1; ++i) {
-      char* dst = buf + (i * rows::NKV + wave) * rows::ROW_BYTES;
+      char* dst = buf + (i * 4 + wave) * rows::ROW_BYTES;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (rows::lds_void*)dst, 16, int(ro.v[i]), 0, 0, POLICY);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (rows::lds_void*)(dst + rows::TILE_BYTES), 16, int(ro.v[i]), 0,
                                                0, POLICY);
@@ -1115,17 +1167,16 @@ __device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& 
     const char* vg = uniform_ptr(reinterpret_cast<const char*>(p.v_cache + off));
 #pragma unroll
     for (int i = I0; i < I1; ++i) {
-      const int r = i * rows::NKV + wave;
-      const int t = d.T0 + r;
-      const uint32_t gc = uint32_t(lane ^ rows::swz(r));
-      const char* ks = kg + (r * tok_bytes + (gc << 4));
-      const char* vs = vg + (r * tok_bytes + (gc << 4));
+      const int r = i * 4 + wave;
+      const LaneSrc<G> ls = lane_src<G>(r, lane);
+      const int t = d.T0 + ls.tt;
+      const char* ks = kg + ro.v[i];
+      const char* vs = vg + ro.v[i];
       if (t >= d.c && t < d.L) {
         const int jn = t - d.c;
-        const int hh = d.g * rows::NKV + int(gc >> 4);
-        const int w8 = int(gc & 15) * 8;
-        ks = reinterpret_cast<const char*>(p.k_new + d.b * p.kn_sb + jn * p.kn_ss + hh * p.kn_sh + w8);
-        vs = reinterpret_cast<const char*>(p.v_new + d.b * p.vn_sb + jn * p.vn_ss + hh * p.vn_sh + w8);
+        const int hh = d.g * G::HG + ls.hg;
+        ks = reinterpret_cast<const char*>(p.k_new + d.b * p.kn_sb + jn * p.kn_ss + hh * p.kn_sh + 8 * ls.cc);
+        vs = reinterpret_cast<const char*>(p.v_new + d.b * p.vn_sb + jn * p.vn_ss + hh * p.vn_sh + 8 * ls.cc);
       }
       __builtin_amdgcn_global_load_lds(ks, (rows::lds_void*)(buf + r * rows::ROW_BYTES), 16, 0, POLICY);
       __builtin_amdgcn_global_load_lds(vs, (rows::lds_void*)(buf + rows::TILE_BYTES + r * rows::ROW_BYTES), 16, 0,
@@ -1134,21 +1185,27 @@ __device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& 
   }
   if (with_q) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 4 * i + (lane >> 4);
+    for (int i = 0; i < G::Q_COPIES; ++i) {
+      const int qi = wave * G::Q_COPIES + i;                      // 1 KiB piece of the Q area
+      const int ar = qi * (1024 / G::QROW) + lane / G::QCH;       // area row: head hq_g, query row rr
+      const int hq_g = ar / 16;
+      const int row = ar % 16;
       const int rr = min(row, p.R - 1);
       const int jq = rr / p.g;
       const int hq = rr - jq * p.g;
-      const int gq = (lane & 15) ^ (row & 15);
-      const uint16_t* src = p.q + d.b * p.q_sb + jq * p.q_ss + ((d.g * rows::NKV + wave) * p.g + hq) * p.q_sh + gq * 8;
-      __builtin_amdgcn_global_load_lds(src, (rows::lds_void*)(buf + 2 * rows::TILE_BYTES + (wave * 16 + 4 * i) * 256),
-                                       16, 0, 0);
+      const int gq = (lane % G::QCH) ^ (row % G::QCH);
+      const uint16_t* src =
+          p.q + d.b * p.q_sb + jq * p.q_ss + ((d.g * G::HG + hq_g) * p.g + hq) * p.q_sh + gq * 8;
+      __builtin_amdgcn_global_load_lds(src, (rows::lds_void*)(buf + 2 * rows::TILE_BYTES + qi * 1024), 16, 0, 0);
     }
   }
 }
 
-// Head-h MFMA operands of the tile in LDS buffer `buf` into registers (same layout as load_tile).
-__device__ __forceinline__ void rows_read_tile(const char* buf, int h, int T0, int t_end, KVTile<128>& tl) {
+// MFMA operands of subtile s of wave w's slice of the tile in LDS buffer `buf` (load_tile's
+// register layout); T0s is the subtile's first token, V rows at or past t_end read as zero.
+template <typename G>
+__device__ __forceinline__ void rows_read_tile(const char* buf, int w, int s, int T0s, int t_end,
+                                               KVTile<G::HD>& tl) {
   const int lane = threadIdx.x & 63;
   const int li = lane & 15;
   const int lq = lane >> 4;
@@ -1156,8 +1213,8 @@ __device__ __forceinline__ void rows_read_tile(const char* buf, int h, int T0, i
   for (int a = 0; a < 2; ++a) {
     const int r = 8 * (li >> 2) + 4 * a + (li & 3);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int chunk = h * 16 + ((4 * kk + lq) ^ rows::swz(r));
+    for (int kk = 0; kk < G::HD / 32; ++kk) {
+      const int chunk = w * 16 + ((s * G::SCH + 4 * kk + lq) ^ rows::swz(r));
       tl.kr[a][kk] = *reinterpret_cast<const u32x4*>(buf + r * rows::ROW_BYTES + chunk * 16);
     }
   }
@@ -1165,57 +1222,74 @@ __device__ __forceinline__ void rows_read_tile(const char* buf, int h, int T0, i
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int r = 8 * lq + e;
-    const int chunk = h * 16 + (li ^ rows::swz(r));
-    const u32x4 v = *reinterpret_cast<const u32x4*>(vb + r * rows::ROW_BYTES + chunk * 16);
-    const bool keep = T0 + r < t_end;  // rows past the sequence: P = 0 must not meet a stale NaN
-    tl.vr[e].w[0] = keep ? v[0] : 0u;
-    tl.vr[e].w[1] = keep ? v[1] : 0u;
-    tl.vr[e].w[2] = keep ? v[2] : 0u;
-    tl.vr[e].w[3] = keep ? v[3] : 0u;
+    const bool keep = T0s + r < t_end;  // rows past the sequence: P = 0 must not meet a stale NaN
+    if constexpr (G::HD == 128) {
+      const int chunk = w * 16 + (li ^ rows::swz(r));
+      const u32x4 v = *reinterpret_cast<const u32x4*>(vb + r * rows::ROW_BYTES + chunk * 16);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) tl.vr[e].w[k] = keep ? v[k] : 0u;
+    } else {
+      const int chunk = w * 16 + ((s * G::SCH + (li >> 1)) ^ rows::swz(r));
+      const u32x2 v = *reinterpret_cast<const u32x2*>(vb + r * rows::ROW_BYTES + chunk * 16 + (li & 1) * 8);
+      tl.vr[e].w[0] = keep ? v[0] : 0u;
+      tl.vr[e].w[1] = keep ? v[1] : 0u;
+    }
   }
 }
 
-// Q^T operand (load_q's layout) of head h's rows from the buffer's Q area; rows li >= R get 0.
-__device__ __forceinline__ void rows_read_q(const AttnParams& p, const char* buf, int h, bf16x8 (&qf)[1][4]) {
+// Q^T operand (load_q's layout) of group head hg's rows from the buffer's Q area; rows li >= R
+// get 0.
+template <typename G>
+__device__ __forceinline__ void rows_read_q(const AttnParams& p, const char* buf, int hg,
+                                            bf16x8 (&qf)[1][G::HD / 32]) {
   const int lane = threadIdx.x & 63;
   const int li = lane & 15;
   const int lq = lane >> 4;
-  const char* qa = buf + 2 * rows::TILE_BYTES + (h * 16 + li) * 256;
+  const char* qa = buf + 2 * rows::TILE_BYTES + (hg * 16 + li) * G::QROW;
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(qa + (((lq + 4 * kk) ^ li) << 4));
+  for (int kk = 0; kk < G::HD / 32; ++kk) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(qa + (((lq + 4 * kk) ^ (li % G::QCH)) << 4));
     qf[0][kk] = __builtin_bit_cast(bf16x8, li < p.R ? v : u32x4{0u, 0u, 0u, 0u});
   }
 }
 
-// Append: store head h's slice of the new rows of tile d, already in LDS buffer `buf`, to the
-// cache (a page id outside the pool was flagged and is skipped).
+// Append: wave w stores its slice of the new rows of tile d (head hg, its phase's tokens),
+// already in LDS buffer `buf`, to the cache (a page id outside the pool was flagged and is
+// skipped).
+template <typename G>
 __device__ __forceinline__ void rows_append_from_lds(const AttnParams& p, const TileDesc& d, const char* buf) {
   if (d.pid < 0) return;
   const int lane = threadIdx.x & 63;
-  const int h = threadIdx.x >> 6;
-  const int li = lane & 15;
-  const int lq = lane >> 4;
-  const int t_lo = max(d.T0, d.c);
-  const int t_hi = min(d.T0 + rows::TILE, d.L);
-  for (int t0 = t_lo; t0 < t_hi; t0 += 4) {
-    const int t = t0 + lq;
-    if (t < t_hi) {
-      const int r = t - d.T0;
-      const int pos = (h * 16 + (li ^ rows::swz(r))) * 16;
-      const u32x4 kv = *reinterpret_cast<const u32x4*>(buf + r * rows::ROW_BYTES + pos);
-      const u32x4 vv = *reinterpret_cast<const u32x4*>(buf + rows::TILE_BYTES + r * rows::ROW_BYTES + pos);
-      const int64_t dst = int64_t(d.pid) * p.page_stride + int64_t(t & ((1 << p.log2_page) - 1)) * p.tok_elems +
-                          (d.g * rows::NKV + h) * rows::HD + 8 * li;
-      st16(p.k_cache + dst, kv);
-      st16(p.v_cache + dst, vv);
+  const int w = threadIdx.x >> 6;
+  const int hg = w % G::HG;
+  const int ph = w / G::HG;
+  constexpr int RPP = 64 / G::SCH;  // token rows per pass
+  const int ch = lane % G::SCH;
+#pragma unroll
+  for (int s = 0; s < G::S; ++s) {
+    const int T0s = d.T0 + rows::TILE * (ph * G::S + s);
+    const int t_lo = max(T0s, d.c);
+    const int t_hi = min(T0s + rows::TILE, d.L);
+    for (int t0 = t_lo; t0 < t_hi; t0 += RPP) {
+      const int t = t0 + lane / G::SCH;
+      if (t < t_hi) {
+        const int r = t - T0s;
+        const int pos = (w * 16 + ((s * G::SCH + ch) ^ rows::swz(r))) * 16;
+        const u32x4 kv = *reinterpret_cast<const u32x4*>(buf + r * rows::ROW_BYTES + pos);
+        const u32x4 vv = *reinterpret_cast<const u32x4*>(buf + rows::TILE_BYTES + r * rows::ROW_BYTES + pos);
+        const int64_t dst = int64_t(d.pid) * p.page_stride + int64_t(t & ((1 << p.log2_page) - 1)) * p.tok_elems +
+                            (d.g * G::HG + hg) * G::HD + 8 * ch;
+        st16(p.k_cache + dst, kv);
+        st16(p.v_cache + dst, vv);
+      }
     }
   }
 }
 
 // s_waitcnt vmcnt(n) for a wave-uniform n, rounded down to a multiple of 4 (a stricter wait) and
 // capped at 60: the immediate must be a constant, so the count selects among the encodings
-// (vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt fields left at "no wait").
+// (vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt fields left at "no wait").  (An exact wait,
+// one encoding per count, measured 6.5 us slower per config-5 verify call and no faster on decode.)
 __device__ __forceinline__ void wait_vmcnt_at_most(int n) {
 #define PKV_VMCNT_CASE(k) \
   case k: __builtin_amdgcn_s_waitcnt(0x0F70 | ((4 * k) & 15) | (((4 * k) >> 4) << 14)); break;
@@ -1230,8 +1304,9 @@ __device__ __forceinline__ void wait_vmcnt_at_most(int n) {
 
 // Q^T operand of head h's 16*NT rows of sequence d.b straight from q into registers (load_q's
 // layout; rows >= R get zeros).  Used where NT > 1, whose Q does not fit the LDS buffers.
-template <int NT>
-__device__ __forceinline__ void rows_load_q(const AttnParams& p, const TileDesc& d, int h, bf16x8 (&qf)[NT][4]) {
+template <int HD, int NT>
+__device__ __forceinline__ void rows_load_q(const AttnParams& p, const TileDesc& d, int h,
+                                            bf16x8 (&qf)[NT][HD / 32]) {
   const int lane = threadIdx.x & 63;
   const int li = lane & 15;
   const int lq = lane >> 4;
@@ -1243,7 +1318,7 @@ __device__ __forceinline__ void rows_load_q(const AttnParams& p, const TileDesc&
     const int hq = rc - jq * p.g;
     const uint16_t* base = p.q + d.b * p.q_sb + jq * p.q_ss + (h * p.g + hq) * p.q_sh + 8 * lq;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
+    for (int kk = 0; kk < HD / 32; ++kk) {
       const u32x4 v = ld16(base + 32 * kk);
       qf[nt][kk] = __builtin_bit_cast(bf16x8, rr < p.R ? v : u32x4{0u, 0u, 0u, 0u});
     }
@@ -1267,11 +1342,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(const AttnParams& p) {
 }
 // Stores of one (row, lane) share of an fp16 partial and its log-sum-exp with cache policy POL:
 // device-coherent (kCoherent) when the merge runs inside the launch, plain for the two-pass merge.
-template <int POL>
-__device__ __forceinline__ void ws_store_partial(__amdgpu_buffer_rsrc_t rs, uint32_t o_off, const u32x4 (&ov)[4],
-                                                 bool with_lse, uint32_t lse_off, float lse) {
+// ov[r]: the lane's DPL head-dim elements of accumulator row r as fp16 pairs (DPL / 2 words).
+template <int POL, int DPL>
+__device__ __forceinline__ void ws_store_partial(__amdgpu_buffer_rsrc_t rs, uint32_t o_off,
+                                                 const uint32_t (&ov)[4][DPL / 2], bool with_lse, uint32_t lse_off,
+                                                 float lse) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) __builtin_amdgcn_raw_buffer_store_b128(ov[r], rs, int(o_off + 16u * r), 0, POL);
+  for (int r = 0; r < 4; ++r) {
+    if constexpr (DPL == 8)
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{ov[r][0], ov[r][1], ov[r][2], ov[r][3]}, rs,
+                                             int(o_off + 16u * r), 0, POL);
+    else
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2{ov[r][0], ov[r][1]}, rs, int(o_off + 8u * r), 0, POL);
+  }
   if (with_lse) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, lse), rs, int(lse_off), 0, POL);
 }
 
@@ -1282,7 +1365,7 @@ struct SeqParts {
   int np, w0, slot0;
 };
 
-template <int NCH>
+template <int NCH, int TOK>
 __device__ __forceinline__ SeqParts seq_parts(const AttnParams& p, const SeqTable<NCH>& st, int b, int base, int per) {
   int first = 0, L = 0;
 #pragma unroll
@@ -1295,16 +1378,16 @@ __device__ __forceinline__ SeqParts seq_parts(const AttnParams& p, const SeqTabl
   first += base;  // the group's first tile
   SeqParts sp;
   sp.w0 = first / per;
-  sp.np = (first + seq_tiles(p, L) - 1) / per - sp.w0 + 1;
+  sp.np = (first + seq_tiles<TOK>(p, L) - 1) / per - sp.w0 + 1;
   sp.slot0 = 2 * sp.w0 + (first != sp.w0 * per ? 1 : 0);
   return sp;
 }
 
-// A split-K partial of (workspace slot, KV head): per query row, O / l as fp16 (16 B per 8
-// head-dim elements; O / l is a convex combination of V rows, so fp16's range and 2^-11 rounding
-// are ample next to the bf16 output) and its log-sum-exp lse = m + log2(l) in fp32 (-inf when
-// the row saw no key).  O of row r: byte (((slot * 4 + h) * R + r) * head_dim) * 2 from ws_o;
-// lse: float ((slot * 4 + h) * R + r) from ws_ml.
+// A split-K partial of (workspace slot, KV head h of the group): per query row, O / l as fp16
+// (16 B per 8 head-dim elements; O / l is a convex combination of V rows, so fp16's range and
+// 2^-11 rounding are ample next to the bf16 output) and its log-sum-exp lse = m + log2(l) in fp32
+// (-inf when the row saw no key).  O of row r: byte (((slot * HG + h) * R + r) * head_dim) * 2
+// from ws_o; lse: float ((slot * HG + h) * R + r) from ws_ml.
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));  // RNE
@@ -1324,200 +1407,299 @@ __device__ __forceinline__ void unpack_f16x8(const u32x4 v, float (&f)[8]) {
   }
 }
 
-// Log-sum-exp merge of the np partials of (b, KV head h) into the bf16 output, by one wave, with
-// the parts read straight from the workspace into registers (device-coherent buffer loads).
-// Lane l owns the 16-byte chunks i = l + 64 c (c < NC) of the R x head_dim block: row i / 16,
-// head-dim elements 8 (i % 16) .. + 7.  Parts go in windows of at most KW (as many as the LDS
-// area holds log-sum-exps for; one window unless np * R is in the thousands):
-//   1. every lane loads some of the window's log-sum-exps into the area, row-major [r][k];
-//   2. lane r < R turns row r's into weights exp2(lse - M) against the running max M, rescales
-//      the running sum and publishes the factor that rescales what was accumulated so far;
-//   3. every lane accumulates its chunks over the window's parts, PB parts per batch, the next
-//      batch's loads in flight during this one's FMAs (2 PB NC 16-byte loads outstanding per
-//      lane at most: beyond ~24 the latency of such loads rises tenfold).
-// No loop body reads LDS in a dependent chain: a lane's weights come four at a time.
-template <int NC>
-__device__ __forceinline__ void merge_parts(const AttnParams& p, int b, int h, int hout, const SeqParts& sp,
-                                            float* area, int area_floats) {
-  constexpr int HD = rows::HD;
-  constexpr int PB = NC >= 8 ? 1 : 8 / NC;
+// Butterfly max / sum over all 64 lanes without LDS: DPP swaps inside each 16-lane row, then the
+// row swaps of max_over_quads / sum_over_quads.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false)));   // lane ^ 1
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false)));   // lane ^ 2
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false)));  // half-row mirror
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xf, 0xf, false)));  // row mirror
+  return max_over_quads(v);
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xf, 0xf, false));
+  return sum_over_quads(v);
+}
+
+// Log-sum-exp merge of query rows rr[0 .. NR) of (sequence b, KV head hk; rr[q] < 0: none) over
+// n_parts split-K partials (part u of row r at workspace row row_of(u, r)) into the bf16 output,
+// by one wave.  The merge is
+// latency-bound, so everything one round trip can fetch is fetched at once, for up to 64 parts:
+// lane u loads part u's log-sum-exp, and lane (g, c) = (lane / CPR, lane % CPR) loads the 16 bytes
+// of head-dim chunk c (elements 8c .. 8c + 7; CPR = head_dim / 8 chunks per row) of parts g,
+// g + PG, g + 2 PG, ... of the row (PG = 64 / CPR part groups; 16 or 8 loads in flight per lane:
+// one round trip for 64 parts, where 4-byte loads needed one per 8).  Weights reach the lanes by
+// ds_bpermute, the part groups are summed with lane swaps, and lanes of group 0 store the row.
+// No LDS, no barrier; loops stay rolled where the code would otherwise grow (every launch starts
+// from a cold instruction cache).  COH: device-coherent loads (partials written during this
+// launch, by workgroups on any XCD).
+constexpr int kLeanMergeParts = 64;
+
+template <typename G, bool COH, int NR, typename RowOf>
+__device__ __forceinline__ void merge_rows(const AttnParams& p, int hk, int b, const int (&rr)[NR], int n_parts,
+                                           RowOf row_of) {
+  constexpr int HD = G::HD;
+  constexpr int CPR = HD / 8;   // 16-byte chunks per part row
+  constexpr int PG = 64 / CPR;  // part groups
   const int lane = threadIdx.x & 63;
-  const int R = p.R;
-  const int nch = R * (HD / 8);
-  // weights [r][k] with a row pitch KWP (a multiple of 4), then per-row rescale and 1 / sum
-  const int KWP = min(((sp.np + 3) & ~3), ((area_floats - 2 * R) / R) & ~3);
-  float* wts = area;
-  float* resc = area + R * KWP;
-  float* rinv = resc + R;
+  const int pg = lane / CPR;
+  const int dc = lane % CPR;
   const __amdgpu_buffer_rsrc_t rs = ws_rsrc(p);
   const uint32_t lse0 = uint32_t(p.ws_ml - p.ws_o) * 4u;
-  auto part_row0 = [&](int k) -> uint32_t {
-    const int slot = k == 0 ? sp.slot0 : 2 * (sp.w0 + k);
-    return uint32_t((slot * rows::NKV + h) * R);
+  const char* o16 = reinterpret_cast<const char*>(p.ws_o);  // fp16 rows of HD * 2 bytes
+  float M_run[NR], S_run[NR];
+  float acc[NR][8];
+#pragma unroll
+  for (int q = 0; q < NR; ++q) {
+    M_run[q] = -INFINITY;
+    S_run[q] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[q][e] = 0.f;
+  }
+  // parts u0 .. u0 + nb - 1 (nb <= PG KP) of every row: every load at once, then the weights and
+  // the sums (rows with rr[q] < 0 are skipped)
+  auto batch = [&](auto kp, int u0, int nb) {
+    constexpr int KP = decltype(kp)::value;
+    float lse[NR];
+    u32x4 x[NR][KP];
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+      lse[q] = -INFINITY;
+      if (rr[q] >= 0 && lane < nb) {
+        const int64_t row = row_of(u0 + lane, rr[q]);
+        if constexpr (COH)
+          lse[q] = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(rs, int(lse0 + uint32_t(row) * 4u), 0, kCoherent));
+        else
+          lse[q] = p.ws_ml[row];
+      }
+#pragma unroll
+      for (int k = 0; k < KP; ++k) {
+        const int part = PG * k + pg;
+        x[q][k] = u32x4{0u, 0u, 0u, 0u};
+        if (rr[q] >= 0 && part < nb) {
+          const int64_t row = row_of(u0 + part, rr[q]);
+          if constexpr (COH)
+            x[q][k] = __builtin_amdgcn_raw_buffer_load_b128(rs, int(uint32_t(row) * (HD * 2) + dc * 16), 0, kCoherent);
+          else
+            x[q][k] = ld16(o16 + row * (HD * 2) + dc * 16);
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+      const float M_new = fmaxf(M_run[q], wave_max(lse[q]));
+      const float M_use = (M_new == -INFINITY) ? 0.f : M_new;
+      const float w = fast_exp2(lse[q] - M_use);  // 0 for lanes past the batch
+      const float resc = fast_exp2(M_run[q] - M_use);
+      S_run[q] = S_run[q] * resc + wave_sum(w);
+      M_run[q] = M_new;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[q][e] *= resc;
+#pragma unroll
+      for (int k = 0; k < KP; ++k) {
+        const float wk = __shfl(w, PG * k + pg, 64);
+        float f[8];
+        unpack_f16x8(x[q][k], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[q][e] += wk * f[e];
+      }
+    }
   };
-  int rowc[NC];
-  bool okc[NC];
-  float acc[NC][8];
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int i = lane + 64 * c;
-    okc[c] = i < nch;
-    rowc[c] = (okc[c] ? i : 0) >> 4;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[c][e] = 0.f;
+  if (n_parts <= 8) {
+    batch(std::integral_constant<int, 8 / PG>(), 0, n_parts);
+  } else {
+#pragma unroll 1
+    for (int u0 = 0; u0 < n_parts; u0 += kLeanMergeParts)
+      batch(std::integral_constant<int, kLeanMergeParts / PG>(), u0, min(kLeanMergeParts, n_parts - u0));
   }
-  float M = -INFINITY, S = 0.f;  // lanes r < R: row r's running max and sum of weights
-  for (int k0 = 0; k0 < sp.np; k0 += KWP) {
-    const int nk = min(KWP, sp.np - k0);
-    // 1. log-sum-exps, -inf past the window's parts
-    for (int e = lane; e < R * KWP; e += 64) {
-      const int r = e / KWP;
-      const int k = e - r * KWP;
-      float v = -INFINITY;
-      if (k < nk)
-        v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                          rs, int(lse0 + (part_row0(k0 + k) + r) * 4u), 0, kCoherent));
-      wts[e] = v;
+#pragma unroll
+  for (int q = 0; q < NR; ++q) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if constexpr (PG == 8) acc[q][e] += __shfl_xor(acc[q][e], 8, 64);
+      acc[q][e] = sum_over_quads(acc[q][e]);
     }
-    // 2. weights (this wave's own LDS writes complete before its later LDS reads)
-    if (lane < R) {
-      float* wr = wts + lane * KWP;
-      float Mn = M;
-      for (int k = 0; k < nk; k += 4) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(wr + k);
-        Mn = fmaxf(Mn, fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
-      }
-      const float Mu = Mn == -INFINITY ? 0.f : Mn;
-      const float f = fast_exp2(M - Mu);  // 0 while nothing was accumulated (M = -inf)
-      S *= f;
-      for (int k = 0; k < nk; k += 4) {
-        f32x4 v = *reinterpret_cast<const f32x4*>(wr + k);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          v[q] = fast_exp2(v[q] - Mu);
-          S += v[q];
-        }
-        *reinterpret_cast<f32x4*>(wr + k) = v;
-      }
-      resc[lane] = f;
-      M = Mn;
-    }
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const float f = resc[rowc[c]];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[c][e] *= f;
-    }
-    // 3. the window's parts
-    u32x4 xa[PB][NC], xb[PB][NC];
-    auto load = [&](u32x4 (&x)[PB][NC], int kb) {
-#pragma unroll
-      for (int kk = 0; kk < PB; ++kk) {
-        const int k = kb + kk;
-        const uint32_t base = part_row0(k0 + (k < nk ? k : 0)) * uint32_t(HD * 2);
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          x[kk][c] = u32x4{0u, 0u, 0u, 0u};
-          if (k < nk && okc[c])
-            x[kk][c] = __builtin_amdgcn_raw_buffer_load_b128(rs, int(base + uint32_t(lane + 64 * c) * 16u), 0,
-                                                             kCoherent);
-        }
-      }
-    };
-    auto accum = [&](const u32x4 (&x)[PB][NC], int kb) {
-#pragma unroll
-      for (int kk = 0; kk < PB; ++kk) {
-        const int k = kb + kk;
-        if (k < nk) {
-#pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            const float wt = wts[rowc[c] * KWP + k];
-            float f[8];
-            unpack_f16x8(x[kk][c], f);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[c][e] += wt * f[e];
-          }
-        }
-      }
-    };
-    load(xa, 0);
-    for (int kb = 0; kb < nk; kb += 2 * PB) {
-      if (kb + PB < nk) load(xb, kb + PB);
-      accum(xa, kb);
-      if (kb + PB >= nk) break;
-      if (kb + 2 * PB < nk) load(xa, kb + 2 * PB);
-      accum(xb, kb + PB);
-    }
-  }
-  if (lane < R) rinv[lane] = S > 0.f ? 1.f / S : 0.f;
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    if (okc[c]) {
-      const int i = lane + 64 * c;
-      const int row = rowc[c];
-      const float inv = rinv[row];
-      const int j = row / p.g;
-      const int hq = row - j * p.g;
+    if (pg == 0 && rr[q] >= 0) {
+      const float inv = S_run[q] > 0.f ? 1.f / S_run[q] : 0.f;
+      const int j = rr[q] / p.g;
+      const int hq = rr[q] - j * p.g;
       u32x4 ov;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[c][2 * k] * inv, acc[c][2 * k + 1] * inv);
-      st16(p.out + b * p.o_sb + j * p.o_ss + (hout * p.g + hq) * p.o_sh + 8 * (i & 15), ov);
+      for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[q][2 * k] * inv, acc[q][2 * k + 1] * inv);
+      st16(p.out + b * p.o_sb + j * p.o_ss + (hk * p.g + hq) * p.o_sh + 8 * dc, ov);
     }
   }
 }
 
-// merge_parts for the row count of the launch (chunks per lane: R * 16 / 64, rounded up).
-template <int NT>
-__device__ __forceinline__ void merge_parts_for(const AttnParams& p, int b, int h, int hout, const SeqParts& sp,
-                                                float* area, int area_floats) {
-  if constexpr (NT == 1) {
-    if (p.R <= 4)
-      merge_parts<1>(p, b, h, hout, sp, area, area_floats);
-    else if (p.R <= 8)
-      merge_parts<2>(p, b, h, hout, sp, area, area_floats);
-    else
-      merge_parts<4>(p, b, h, hout, sp, area, area_floats);
-  } else {
-    merge_parts<4 * NT>(p, b, h, hout, sp, area, area_floats);
+// The in-launch merge (decode rows, R <= 16).  Workgroups lean_grid, lean_grid + 1, ... of a
+// balanced launch merge the partials of (sequence b, KV head hk, query rows 4 rq .. 4 rq + 3),
+// one wave per row (two rows per wave, with half the workgroups, measured no faster): they wait
+// for (sequence, head)'s arrival counter to reach the part count, then merge with merge_rows.  Every XCD dispatches its workgroups in order, so these start only
+// on CUs that decode workgroups of lower index (which never wait) have left or never needed: a
+// merge workgroup waits only for workgroups that are already running.  The wait is bounded
+// (kMergeSpinLimit polls; beyond it the wave flags PKV_STATUS_MERGE_TIMEOUT and leaves), so
+// every wave exits.  The counter's low 16 bits count arrived parts; each of the row groups'
+// workgroups adds 1 << 16 once it has read them, and the last to do so re-arms it at zero.
+#ifndef PKV_MERGE_SPIN_LIMIT
+#define PKV_MERGE_SPIN_LIMIT (1 << 20)
+#endif
+constexpr int kMergeSpinLimit = PKV_MERGE_SPIN_LIMIT;
+
+template <typename G, int NCH>
+__device__ __forceinline__ void merge_workgroup(const AttnParams& p, const SeqTable<NCH>& st, int T1, int per,
+                                                int* ready_s) {
+  const int m = int(blockIdx.x) - p.lean_grid;
+  const int n_rq = (p.R + 3) / 4;
+  const int hk = m % p.n_kv;
+  const int rq = (m / p.n_kv) % n_rq;
+  const int b = m / (p.n_kv * n_rq);
+  if (b >= p.batch) return;
+  const int g = hk / G::HG;
+  const int h = hk - g * G::HG;
+  const SeqParts sp = seq_parts<NCH, G::TOK>(p, st, b, g * T1, per);
+  if (sp.np <= 1) return;  // the sequence lies in one range: its output is written already
+  int* cnt = p.ws_cnt + ((g * p.batch + b) * G::HG + h) * p.cnt_stride;
+  // one poller per workgroup (every poll is a device-coherent load of a line that the arrivals
+  // update; more pollers only queue behind each other and the arrivals), the others wait at the
+  // barrier (ready_s: a word of the launch's LDS, which merge workgroups use for nothing else)
+  if (threadIdx.x == 0) {
+    int seen = 0;
+    for (int i = 0; i < kMergeSpinLimit; ++i) {
+      seen = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((seen & 0xffff) >= sp.np) break;
+      __builtin_amdgcn_s_sleep(4);
+    }
+    *ready_s = (seen & 0xffff) >= sp.np;
+    if (!*ready_s) flag_status(p.status, PKV_STATUS_MERGE_TIMEOUT);
+  }
+  __syncthreads();
+  const bool ready = *ready_s;
+  const int r0 = 4 * rq + int(threadIdx.x >> 6);
+  const int rr[1] = {r0 < p.R ? r0 : -1};
+  if (ready && rr[0] >= 0)
+    merge_rows<G, true, 1>(p, hk, b, rr, sp.np, [&](int part, int r) -> int64_t {
+      const int slot = part == 0 ? sp.slot0 : 2 * (sp.w0 + part);
+      return (int64_t(slot) * G::HG + h) * p.R + r;
+    });
+  __syncthreads();  // every wave of this workgroup has read its parts
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(cnt, 1 << 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == (((n_rq - 1) << 16) | sp.np)) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
-template <int NT, int NCH, bool CASCADE_SUFFIX>
+// Phase merge at the end of a segment (geometries with P > 1): the waves of phases 1 .. P-1
+// publish their softmax state (m, the lane's partial l, O) for their head in the K/V area of
+// the tile buffer `buf` just consumed (its next copies are issued only after this), and the
+// phase-0 wave of each head folds them into its own; as many states per round as the 64 KiB
+// area holds, lane-major so every access is conflict-free.  Every wave of the workgroup calls it.
+template <typename G, int NT>
+__device__ __forceinline__ void phase_merge(char* buf, float (&m_run)[NT], float (&l_run)[NT],
+                                            f32x4 (&acc)[NT][G::HD / 16]) {
+  constexpr int DPL = G::HD / 16;
+  constexpr int FPL = NT * (4 * DPL + 2);  // floats of one lane's state
+  constexpr int SLOTS = (2 * rows::TILE_BYTES / 4) / (FPL * 64);
+  static_assert(SLOTS >= 1, "a wave state must fit the tile buffer");
+  constexpr int WRITERS = (G::P - 1) * G::HG;
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int k = w - G::HG;  // writer index of phases >= 1 (wave w = hg + HG ph)
+  float* area = reinterpret_cast<float*>(buf);
+#pragma unroll 1
+  for (int k0 = 0; k0 < WRITERS; k0 += SLOTS) {
+    if (k >= k0 && k < k0 + SLOTS) {
+      float* a = area + (k - k0) * FPL * 64 + lane;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        float* an = a + nt * (4 * DPL + 2) * 64;
+        an[0] = m_run[nt];
+        an[64] = l_run[nt];
+#pragma unroll
+        for (int n = 0; n < DPL; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) an[(2 + 4 * n + r) * 64] = acc[nt][n][r];
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    raw_barrier();
+    if (w < G::HG) {
+#pragma unroll 1
+      for (int kw = w + ((k0 + G::HG - 1 - w) / G::HG) * G::HG; kw < min(WRITERS, k0 + SLOTS); kw += G::HG) {
+        // writer kw: head kw % HG = w
+        const float* a = area + (kw - k0) * FPL * 64 + lane;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const float* an = a + nt * (4 * DPL + 2) * 64;
+          const float mo = an[0];
+          const float lo = an[64];
+          const float M = fmaxf(m_run[nt], mo);
+          const float Mu = M == -INFINITY ? 0.f : M;
+          const float fs = fast_exp2(m_run[nt] - Mu);  // 0 for a state that saw no key
+          const float fo = fast_exp2(mo - Mu);
+          l_run[nt] = l_run[nt] * fs + lo * fo;
+#pragma unroll
+          for (int n = 0; n < DPL; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[nt][n][r] = acc[nt][n][r] * fs + an[(2 + 4 * n + r) * 64] * fo;
+          m_run[nt] = M;
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    raw_barrier();
+  }
+}
+
+template <int NT, int NCH, bool CASCADE_SUFFIX, typename G>
 __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p) {
-  constexpr int HD = rows::HD;
+  constexpr int HD = G::HD;
   constexpr int DPL = HD / 16;
+  constexpr int KK = HD / 32;
+  constexpr int TOK = G::TOK;
   constexpr bool kQInLds = NT == 1;
-  constexpr int BUF = kQInLds ? rows::BUF_BYTES : 2 * rows::TILE_BYTES;
+  constexpr int kQCopies = kQInLds ? G::Q_COPIES : 0;
+  constexpr int BUF = 2 * rows::TILE_BYTES + (kQInLds ? G::Q_BYTES : 0);  // K tile | V tile | Q
   constexpr int kPolicy = NT == 1 || CASCADE_SUFFIX ? rows::kStreamPolicy : rows::kVerifyPolicy;
   __shared__ __attribute__((aligned(16))) char lds[2 * BUF];
 
   const int lane = threadIdx.x & 63;
-  const int h = threadIdx.x >> 6;  // one wave per KV head
+  const int w = threadIdx.x >> 6;
+  const int hg = w % G::HG;  // KV head within the group
+  const int ph = w / G::HG;  // phase: keys [32 S ph, 32 S (ph + 1)) of every tile
+  const bool leader = ph == 0;
   const int li = lane & 15;
   const int lq = lane >> 4;
 
   SeqTable<NCH> st;
-  seq_table(p, st);
+  seq_table<NCH, TOK>(p, st);
   const int T1 = st.total;  // tiles of one head group
   const int total = T1 * p.n_groups;
-  const int per = (total + int(gridDim.x) - 1) / int(gridDim.x);
+  const int per = (total + p.lean_grid - 1) / p.lean_grid;
+  if (int(blockIdx.x) >= p.lean_grid) {
+    if constexpr (NT == 1) merge_workgroup<G, NCH>(p, st, T1, per, reinterpret_cast<int*>(lds));
+    return;
+  }
   const int s = min(int(blockIdx.x) * per, total);
   const int e = min(s + per, total);
   if (s >= e) return;
   const int n = e - s;
 
   TileWin win;
-  tile_window(p, st, s, e, T1, win);
+  tile_window<NCH, TOK>(p, st, s, e, T1, win);
   TileDesc dA = tile_desc(win, s);
   TileDesc dB = dA;
-  const RowOffsets ro = row_offsets(p);
-  rows_issue<kPolicy>(p, dA, kQInLds, lds, ro);
+  const RowOffsets ro = row_offsets<G>(p);
+  rows_issue<G, kPolicy>(p, dA, kQInLds, lds, ro);
   if (n > 1) {
     dB = tile_desc(win, s + 1);
-    rows_issue<kPolicy>(p, dB, kQInLds && dB.T0 == p.k0, lds + BUF, ro);
+    rows_issue<G, kPolicy>(p, dB, kQInLds && dB.T0 == p.k0, lds + BUF, ro);
   }
 
-  bf16x8 qf[NT][HD / 32];
+  bf16x8 qf[NT][KK];
   int lim[NT];
   int lim_min = 0x7fffffff;
   float m_run[NT], l_run[NT];
@@ -1539,21 +1721,21 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     char* buf = lds + (j & 1) * BUF;
     // This wave's copies of tile j have landed once at most the operations issued after them are
     // outstanding (vmcnt retires in order): the epilogue stores of iteration j-2 (issued after
-    // group j), group j+1 (16 row copies, + 4 Q copies when Q goes through LDS and tile j+1
-    // starts a segment) and the epilogue stores of iteration j-1.  Store counts are lower bounds:
-    // the wait is never looser than it must be, and no longer stalls on the next tile after a
-    // segment ends.
+    // group j), group j+1 (16 row copies, + the Q copies when Q goes through LDS and tile j+1
+    // starts a segment) and the epilogue stores of iteration j-1.  Store counts are lower bounds
+    // (the append's stores are left out): the wait is never looser than it must be, and no
+    // longer stalls on the next tile after a segment ends.
     if (j + 1 >= n)
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     else
-      wait_vmcnt_at_most((kQInLds && dB.T0 == p.k0 ? 20 : 16) + stores_prev + stores_prev2);
+      wait_vmcnt_at_most(16 + (dB.T0 == p.k0 ? kQCopies : 0) + stores_prev + stores_prev2);
     raw_barrier();  // ... and every other wave's
     if (j == 0 || d.T0 == p.k0) {
       // a segment starts: its Q operand, row limits and a fresh softmax state
       if constexpr (kQInLds)
-        rows_read_q(p, buf, h, qf);
+        rows_read_q<G>(p, buf, hg, qf);
       else
-        rows_load_q<NT>(p, d, d.g * rows::NKV + h, qf);
+        rows_load_q<HD, NT>(p, d, d.g * G::HG + hg, qf);
       seg_j0 = j;
       seg_T0 = d.T0;
       lim_min = 0x7fffffff;
@@ -1576,11 +1758,17 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
       for (int off = 1; off < 16; off <<= 1) lim_min = min(lim_min, __shfl_xor(lim_min, off, 64));
       lim_min = __builtin_amdgcn_readfirstlane(lim_min);
     }
-    if (tile_has_new(p, d)) rows_append_from_lds(p, d, buf);
-    KVTile<HD> tl;
-    rows_read_tile(buf, h, d.T0, d.L, tl);
+    if (tile_has_new<TOK>(p, d)) rows_append_from_lds<G>(p, d, buf);
+    KVTile<HD> tl[G::S];
+#pragma unroll
+    for (int sub = 0; sub < G::S; ++sub)
+      rows_read_tile<G>(buf, w, sub, d.T0 + rows::TILE * (ph * G::S + sub), d.L, tl[sub]);
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
     raw_barrier();                       // nobody reads this buffer any more
+    const bool seg_end = !(j + 1 < n && d.T0 + TOK < d.L);
+    // With phases, a segment end merges the phase states in this buffer first, and tile j + 2's
+    // copies wait until that is done.
+    const bool defer = G::P > 1 && seg_end;
     // Tile j + 2's copies go out in two halves, one before and one after tile j's compute: this
     // wave's copy issue stalls while earlier copies drain, and the split lets that stall overlap
     // the compute (7B decode 31.0 -> 30.7 us, config-5 verify 77.8 -> 74.5 us per call, against
@@ -1589,30 +1777,39 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     const bool next2 = j + 2 < n;
     if (next2) {
       const int x2 = s + j + 2;
-      if (x2 - win.x0 >= 64) tile_window(p, st, x2, e, T1, win);
+      if (x2 - win.x0 >= 64) tile_window<NCH, TOK>(p, st, x2, e, T1, win);
       d2 = tile_desc(win, x2);
-      rows_issue<kPolicy>(p, d2, false, buf, ro, 0, 4);
+      if (!defer) rows_issue<G, kPolicy>(p, d2, false, buf, ro, 0, 4);
     }
     dA = dB;
     dB = d2;
-    if (d.T0 < d.L) {
-      // verify: the prefill kernel's ILP-ordered tile update (all QK products, then the softmax
-      // of every N tile, then every PV product)
-      if constexpr (NT > 1)
-        compute_tile_prefill<NT>(p, tl, d.T0, qf, lim, lim_min, m_run, l_run, acc);
-      else
-        compute_tile<HD, NT, true>(p, tl, d.T0, qf, lim, lim_min, m_run, l_run, acc);
+#pragma unroll
+    for (int sub = 0; sub < G::S; ++sub) {
+      const int T0s = d.T0 + rows::TILE * (ph * G::S + sub);
+      if (T0s < d.L) {
+        // verify: the prefill kernel's ILP-ordered tile update (all QK products, then the softmax
+        // of every N tile, then every PV product)
+        if constexpr (NT > 1 && HD == 128)
+          compute_tile_prefill<NT>(p, tl[sub], T0s, qf, lim, lim_min, m_run, l_run, acc);
+        else
+          compute_tile<HD, NT, true>(p, tl[sub], T0s, qf, lim, lim_min, m_run, l_run, acc);
+      }
     }
-    if (next2) rows_issue<kPolicy>(p, d2, kQInLds && d2.T0 == p.k0, buf, ro, 4, 8);
+    if (next2 && !defer) rows_issue<G, kPolicy>(p, d2, kQInLds && d2.T0 == p.k0, buf, ro, 4, 8);
 
     stores_prev2 = stores_prev;
     stores_prev = 0;
-    if (j + 1 < n && d.T0 + rows::TILE < d.L) continue;  // the segment goes on
-    // ---- segment epilogue: wave h owns head h's rows li + 16 nt < R (per N tile 4 stores, or
-    // 4 + 1 for a partial; every N tile has a real row) ----
+    if (!seg_end) continue;  // the segment goes on
+    if constexpr (G::P > 1) {
+      phase_merge<G, NT>(buf, m_run, l_run, acc);
+      if (next2) rows_issue<G, kPolicy>(p, d2, kQInLds && d2.T0 == p.k0, buf, ro);
+      if (!leader) continue;  // the phase-0 wave of each head holds the merged state
+    }
+    // ---- segment epilogue: wave (hg, phase 0) owns head hg's rows li + 16 nt < R (per N tile 4
+    // stores, or 4 + 1 for a partial; every N tile has a real row) ----
     // a segment holding the sequence's keys [k0, L) complete: its final output, or in a cascade
     // launch its suffix partial (one slot per sequence: a range may hold several)
-    const bool complete = seg_T0 == p.k0 && d.T0 + rows::TILE >= d.L;
+    const bool complete = seg_T0 == p.k0 && d.T0 + TOK >= d.L;
     const bool whole = complete && !p.cascade_splits;
     stores_prev = (whole ? 4 : 5) * NT;
     float lsum[NT];
@@ -1628,13 +1825,20 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
           const int hq = rr - jr * p.g;
           const float inv = lsum[nt] > 0.f ? 1.f / lsum[nt] : 0.f;
           uint16_t* dst =
-              p.out + d.b * p.o_sb + jr * p.o_ss + ((d.g * rows::NKV + h) * p.g + hq) * p.o_sh + 4 * DPL * lq;
+              p.out + d.b * p.o_sb + jr * p.o_ss + ((d.g * G::HG + hg) * p.g + hq) * p.o_sh + 4 * DPL * lq;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            u32x4 ov;
+            if constexpr (DPL == 8) {
+              u32x4 ov;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[nt][2 * k][r] * inv, acc[nt][2 * k + 1][r] * inv);
-            st16(dst + DPL * r, ov);
+              for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[nt][2 * k][r] * inv, acc[nt][2 * k + 1][r] * inv);
+              st16(dst + DPL * r, ov);
+            } else {
+              u32x2 ov;
+#pragma unroll
+              for (int k = 0; k < 2; ++k) ov[k] = pack_bf16x2(acc[nt][2 * k][r] * inv, acc[nt][2 * k + 1][r] * inv);
+              *reinterpret_cast<u32x2*>(dst + DPL * r) = ov;
+            }
           }
         }
       }
@@ -1658,13 +1862,13 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
       for (int nt = 0; nt < NT; ++nt) {
         const int rr = li + 16 * nt;
         if (rr < p.R) {
-          const uint32_t row = uint32_t((slot * rows::NKV + h) * p.R + rr);
+          const uint32_t row = uint32_t((slot * G::HG + hg) * p.R + rr);
           const float inv = lsum[nt] > 0.f ? 1.f / lsum[nt] : 0.f;
-          u32x4 ov[4];
+          uint32_t ov[4][DPL / 2];
 #pragma unroll
           for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
+            for (int k = 0; k < DPL / 2; ++k) {
               const float lo = acc[nt][2 * k][r] * inv, hi = acc[nt][2 * k + 1][r] * inv;
               ovf |= f16_overflows(lo, hi);
               ov[r][k] = pack_f16x2(lo, hi);
@@ -1672,81 +1876,38 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
           const float lse = lsum[nt] > 0.f ? m_run[nt] + __builtin_amdgcn_logf(lsum[nt]) : -INFINITY;
           const uint32_t o_off = (row * HD + 4 * DPL * lq) * 2u;
           if (p.two_pass)
-            ws_store_partial<0>(rs, o_off, ov, lq == 0, lse0 + row * 4u, lse);
+            ws_store_partial<0, DPL>(rs, o_off, ov, lq == 0, lse0 + row * 4u, lse);
           else
-            ws_store_partial<kCoherent>(rs, o_off, ov, lq == 0, lse0 + row * 4u, lse);
+            ws_store_partial<kCoherent, DPL>(rs, o_off, ov, lq == 0, lse0 + row * 4u, lse);
         }
       }
       if (__any(ovf) && lane == 0) flag_status(p.status, PKV_STATUS_PARTIAL_RANGE);
     }
   }
   if (p.two_pass || (pub_first < 0 && pub_last < 0)) return;
-  // In-launch merge.  Once this wave's partial stores have completed, count its arrival at each
-  // sequence it wrote a part of; the wave that brings a (sequence, head) counter to its part
-  // count merges every part and re-arms the counter for the next call.  Nobody waits.
+  // In-launch merge: once this wave's partial stores have completed (device-coherent), count
+  // its arrival at each (sequence, head) it wrote a part of; a merge workgroup of this launch
+  // waits for the count to reach the part count.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the partial stores are device-visible
-  // the tile buffers are free after the loop: a quarter of them per wave for its merges
-  float* area = reinterpret_cast<float*>(lds + h * (2 * BUF / rows::NKV));
-  // both arrivals in flight together, then the merges this wave completes
-  int prev0 = 0, prev1 = 0;
   if (lane == 0) {
     if (pub_first >= 0)
-      prev0 = __hip_atomic_fetch_add(p.ws_cnt + pub_first * rows::NKV + h, 1, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(p.ws_cnt + (pub_first * G::HG + hg) * p.cnt_stride, 1, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
     if (pub_last >= 0)
-      prev1 = __hip_atomic_fetch_add(p.ws_cnt + pub_last * rows::NKV + h, 1, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(p.ws_cnt + (pub_last * G::HG + hg) * p.cnt_stride, 1, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
   }
-  prev0 = __builtin_amdgcn_readfirstlane(prev0);
-  prev1 = __builtin_amdgcn_readfirstlane(prev1);
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int seg = k == 0 ? pub_first : pub_last;
-    if (seg < 0) continue;
-    const int g = seg / p.batch;
-    const int b = seg - g * p.batch;
-    const SeqParts sp = seq_parts(p, st, b, g * T1, per);
-    if ((k == 0 ? prev0 : prev1) != sp.np - 1) continue;
-    if (lane == 0) __hip_atomic_store(p.ws_cnt + seg * rows::NKV + h, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_parts_for<NT>(p, b, h, g * rows::NKV + h, sp, area, 2 * BUF / rows::NKV / 4);
-  }
-}
-
-// Butterfly max / sum over all 64 lanes without LDS: DPP swaps inside each 16-lane row, then the
-// row swaps of max_over_quads / sum_over_quads.
-__device__ __forceinline__ float wave_max(float v) {
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false)));   // lane ^ 1
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false)));   // lane ^ 2
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false)));  // half-row mirror
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xf, 0xf, false)));  // row mirror
-  return max_over_quads(v);
-}
-__device__ __forceinline__ float wave_sum(float v) {
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xf, 0xf, false));
-  return sum_over_quads(v);
 }
 
 // Two-pass merge (PKV_DECODE_TWO_PASS) of the partials a decode_lean_kernel launch of `grid`
 // workgroups left in the workspace.  Workgroup (KV head, sequence, group of 16 query rows), one
-// wave per query row; only sequences whose tiles span more than one range have partials.  The
-// merge is latency-bound, so everything one round trip can fetch is fetched at once, for up to
-// 64 parts: lane u loads part u's log-sum-exp, and lane (g, c) = (lane / 16, lane % 16) loads the
-// 16 bytes of head-dim chunk c (elements 8c .. 8c + 7) of parts g, g + 4, ..., g + 60 of its row
-// (16 loads in flight per lane: one round trip for 64 parts, where 4-byte loads needed one per 8).
-// Weights reach the lanes by ds_bpermute, the four part groups are summed with the row-swap
-// permutes, and lanes of group 0 store the row.  No LDS, no barrier; loops stay rolled where the
-// code would otherwise grow (every launch starts from a cold instruction cache).
-constexpr int kLeanMergeParts = 64;
-
+// wave per query row (merge_row); only sequences whose tiles span more than one range have
+// partials, and in a cascade launch every sequence has the prefix pass's parts as well.
+template <typename G>
 __global__ __launch_bounds__(1024) void combine_lean_kernel(const AttnParams p, int grid) {
-  constexpr int HD = rows::HD;
-  static_assert(HD == 128, "16 lanes x 16 bytes per part row");
-  const int hg = blockIdx.x;  // KV head; its group's tiles follow those of the groups before it
-  const int g = hg / rows::NKV;
-  const int h = hg - g * rows::NKV;  // head within the group (the partials hold 4 per slot)
+  const int hk = blockIdx.x;  // KV head; its group's tiles follow those of the groups before it
+  const int g = hk / G::HG;
+  const int h = hk - g * G::HG;  // head within the group (the partials hold HG per slot)
   const int b = blockIdx.y;
   const int r = int(blockIdx.z) * 16 + int(threadIdx.x >> 6);  // query row of this wave
   const int lane = threadIdx.x & 63;
@@ -1766,7 +1927,7 @@ __global__ __launch_bounds__(1024) void combine_lean_kernel(const AttnParams p, 
       c = min(max(c, 0), cap);
       Lb = min(c + s_new, cap);
     }
-    const int n = bb < p.batch ? seq_tiles(p, Lb) : 0;
+    const int n = bb < p.batch ? seq_tiles<G::TOK>(p, Lb) : 0;
     const int incl = total + wave_incl_scan(n);
     if (b >= q0 && b < q0 + 64) {
       first = __builtin_amdgcn_readlane(incl - n, b - q0);
@@ -1777,14 +1938,15 @@ __global__ __launch_bounds__(1024) void combine_lean_kernel(const AttnParams p, 
   const int per = (total * p.n_groups + grid - 1) / grid;
   first += g * total;
   const int w0 = first / per;
-  const int np = (first + seq_tiles(p, L) - 1) / per - w0 + 1;
+  const int np = (first + seq_tiles<G::TOK>(p, L) - 1) / per - w0 + 1;
   // cascade: the prefix pass's S parts first, then the sequence's suffix partial(s)
   const int S = p.cascade_splits;
   if (np <= 1 && S == 0) return;
   const int n_parts = S + (np <= 1 ? 1 : np);
   // the first range holds b in its first segment only if b starts exactly at the range start
   const int slot0 = 2 * w0 + (first != w0 * per ? 1 : 0);
-  auto row_of = [&](int part) {
+  const int rr[1] = {r};
+  merge_rows<G, false, 1>(p, hk, b, rr, n_parts, [&](int part, int r) -> int64_t {
     int slot;
     if (part < S) {
       slot = 2 * grid + b * S + part;
@@ -1792,61 +1954,8 @@ __global__ __launch_bounds__(1024) void combine_lean_kernel(const AttnParams p, 
       const int v = part - S;
       slot = np <= 1 ? 2 * grid + p.batch * S + b : (v == 0 ? slot0 : 2 * (w0 + v));
     }
-    return (int64_t(slot) * rows::NKV + h) * p.R + r;
-  };
-  const int pg = lane >> 4;
-  const int dc = lane & 15;
-  const char* o16 = reinterpret_cast<const char*>(p.ws_o);  // fp16 rows of HD * 2 bytes
-  float M_run = -INFINITY, S_run = 0.f;
-  float acc[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-  // parts u0 .. u0 + nb - 1 (nb <= 4 KP): every load at once, then the weights and the sums
-  auto batch = [&](auto kp, int u0, int nb) {
-    constexpr int KP = decltype(kp)::value;
-    const float lse = lane < nb ? p.ws_ml[row_of(u0 + lane)] : -INFINITY;
-    u32x4 x[KP];
-#pragma unroll
-    for (int k = 0; k < KP; ++k) {
-      const int part = 4 * k + pg;
-      x[k] = u32x4{0u, 0u, 0u, 0u};
-      if (part < nb) x[k] = ld16(o16 + row_of(u0 + part) * (HD * 2) + dc * 16);
-    }
-    const float M_new = fmaxf(M_run, wave_max(lse));
-    const float M_use = (M_new == -INFINITY) ? 0.f : M_new;
-    const float w = fast_exp2(lse - M_use);  // 0 for lanes past the batch
-    const float resc = fast_exp2(M_run - M_use);
-    S_run = S_run * resc + wave_sum(w);
-    M_run = M_new;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] *= resc;
-#pragma unroll
-    for (int k = 0; k < KP; ++k) {
-      const float wk = __shfl(w, 4 * k + pg, 64);
-      float f[8];
-      unpack_f16x8(x[k], f);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += wk * f[e];
-    }
-  };
-  if (n_parts <= 8) {
-    batch(std::integral_constant<int, 2>(), 0, n_parts);
-  } else {
-#pragma unroll 1
-    for (int u0 = 0; u0 < n_parts; u0 += kLeanMergeParts)
-      batch(std::integral_constant<int, kLeanMergeParts / 4>(), u0, min(kLeanMergeParts, n_parts - u0));
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = sum_over_quads(acc[e]);
-  if (pg == 0) {
-    const float inv = S_run > 0.f ? 1.f / S_run : 0.f;
-    const int j = r / p.g;
-    const int hq = r - j * p.g;
-    u32x4 ov;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[2 * k] * inv, acc[2 * k + 1] * inv);
-    st16(p.out + b * p.o_sb + j * p.o_ss + (hg * p.g + hq) * p.o_sh + 8 * dc, ov);
-  }
+    return (int64_t(slot) * G::HG + h) * p.R + r;
+  });
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -2418,16 +2527,37 @@ static size_t ws_bytes(int batch, int R, int n_kv, int head_dim, int64_t max_spl
   return kCounterBytes + (ws_floats_o(batch, R, n_kv, head_dim, max_splits) + rows * 2) * sizeof(float);
 }
 
-// decode_lean_kernel covers the 7B decode and verify shapes (head_dim 128, 4 KV heads, pages of
-// >= 32 rows, <= kLeanMaxRows query rows per KV head, <= 256 sequences) and runs there unless the
-// caller fixes split_tokens or asks for decode_kernel (PKV_DECODE_HEADS, PKV_DECODE_FUSED_MERGE).
+// Geometry of the balanced kernel for (head_dim, n_kv): the largest head group of 4, 2 or 1 KV
+// heads that divides n_kv (head_dim 128), or of 4 or 2 (head_dim 64); kGeomNone where there is
+// none.  Its tile holds tokens_per_tile tokens, which must lie in one page.
+enum LeanGeom { kGeomNone, kGeom128x4, kGeom128x2, kGeom128x1, kGeom64x4, kGeom64x2 };
+static LeanGeom lean_geom(int head_dim, int n_kv) {
+  if (head_dim == 128) return n_kv % 4 == 0 ? kGeom128x4 : n_kv % 2 == 0 ? kGeom128x2 : kGeom128x1;
+  if (head_dim == 64) return n_kv % 4 == 0 ? kGeom64x4 : n_kv % 2 == 0 ? kGeom64x2 : kGeomNone;
+  return kGeomNone;
+}
+static int lean_tokens_per_tile(LeanGeom g) {
+  switch (g) {
+    case kGeom128x4: return Geom<128, 4>::TOK;
+    case kGeom128x2: return Geom<128, 2>::TOK;
+    case kGeom128x1: return Geom<128, 1>::TOK;
+    case kGeom64x4: return Geom<64, 4>::TOK;
+    case kGeom64x2: return Geom<64, 2>::TOK;
+    default: return 1 << 30;
+  }
+}
+
+// decode_lean_kernel covers head_dim 128 with any n_kv and head_dim 64 with an even n_kv (pages
+// holding whole tiles, <= kLeanMaxRows query rows per KV head, <= 256 sequences) and runs there
+// unless the caller fixes split_tokens or asks for decode_kernel (PKV_DECODE_HEADS).
 #ifndef PKV_LEAN_MAX_ROWS
 #define PKV_LEAN_MAX_ROWS 64
 #endif
 constexpr int kLeanMaxRows = PKV_LEAN_MAX_ROWS;
 static bool use_lean_kernel(int batch, int head_dim, int n_kv, int R, int page_size, int split_tokens,
                             int32_t flags) {
-  return head_dim == rows::HD && n_kv % rows::NKV == 0 && R <= kLeanMaxRows && page_size >= rows::TILE &&
+  const LeanGeom g = lean_geom(head_dim, n_kv);
+  return g != kGeomNone && R <= kLeanMaxRows && page_size >= lean_tokens_per_tile(g) &&
          batch <= rows::kMaxBatch && int64_t(batch) * n_kv <= kMaxCounters && split_tokens <= 0 &&
          !(flags & PKV_DECODE_HEADS);
 }
@@ -2441,25 +2571,60 @@ static int lean_grid(int32_t flags) {
 // decode_lean_kernel for R query rows per KV head (NT = R / 16 MFMA row tiles, rounded up) and
 // a batch of up to 64 or up to 256 sequences (the sequence table's register chunks: a kernel for
 // small batches carries a quarter of the scan and search code, which every launch fetches cold).
-template <int NT, bool CS>
+// The launch's workgroups: `grid` that decode, then (in-launch merge) one per (sequence, KV head,
+// group of 4 query rows) that merge.
+template <int NT, bool CS, typename G>
 static void launch_lean_nt(const AttnParams& p, int batch, int grid, hipStream_t s) {
+  const int wgs = grid + (p.two_pass ? 0 : batch * p.n_kv * ((p.R + 3) / 4));
   if (batch <= 64)
-    decode_lean_kernel<NT, 1, CS><<<grid, 64 * rows::NKV, 0, s>>>(p);
+    decode_lean_kernel<NT, 1, CS, G><<<wgs, 256, 0, s>>>(p);
   else
-    decode_lean_kernel<NT, rows::kChunks, CS><<<grid, 64 * rows::NKV, 0, s>>>(p);
+    decode_lean_kernel<NT, rows::kChunks, CS, G><<<wgs, 256, 0, s>>>(p);
 }
-static void launch_lean(const AttnParams& p, int R, int batch, int grid, hipStream_t s) {
-  const bool cs = p.cascade_splits > 0;  // the suffix pass of a cascade launch
-  switch ((R + 15) / 16) {
-    case 1: launch_lean_nt<1, false>(p, batch, grid, s); break;
-    case 2: cs ? launch_lean_nt<2, true>(p, batch, grid, s) : launch_lean_nt<2, false>(p, batch, grid, s); break;
-    case 3: cs ? launch_lean_nt<3, true>(p, batch, grid, s) : launch_lean_nt<3, false>(p, batch, grid, s); break;
-    default: cs ? launch_lean_nt<4, true>(p, batch, grid, s) : launch_lean_nt<4, false>(p, batch, grid, s); break;
+// The launch (and the two-pass merge's) for geometry G; the suffix pass of a cascade launch
+// (cascade_splits > 0) exists for the 7B geometry only.
+template <typename G>
+static void launch_lean_g(const AttnParams& p, int R, int batch, int grid, hipStream_t s) {
+  const bool cs = p.cascade_splits > 0;
+  if constexpr (std::is_same<G, Geom7B>::value) {
+    switch ((R + 15) / 16) {
+      case 1: launch_lean_nt<1, false, G>(p, batch, grid, s); break;
+      case 2: cs ? launch_lean_nt<2, true, G>(p, batch, grid, s) : launch_lean_nt<2, false, G>(p, batch, grid, s); break;
+      case 3: cs ? launch_lean_nt<3, true, G>(p, batch, grid, s) : launch_lean_nt<3, false, G>(p, batch, grid, s); break;
+      default: cs ? launch_lean_nt<4, true, G>(p, batch, grid, s) : launch_lean_nt<4, false, G>(p, batch, grid, s); break;
+    }
+  } else {
+    (void)cs;
+    switch ((R + 15) / 16) {
+      case 1: launch_lean_nt<1, false, G>(p, batch, grid, s); break;
+      case 2: launch_lean_nt<2, false, G>(p, batch, grid, s); break;
+      case 3: launch_lean_nt<3, false, G>(p, batch, grid, s); break;
+      default: launch_lean_nt<4, false, G>(p, batch, grid, s); break;
+    }
+  }
+  if (p.two_pass)
+    combine_lean_kernel<G><<<dim3(p.n_kv, batch, (R + 15) / 16), 64 * (R < 16 ? R : 16), 0, s>>>(p, grid);
+}
+static void launch_lean(const AttnParams& p, int head_dim, int R, int batch, int grid, hipStream_t s) {
+  switch (lean_geom(head_dim, p.n_kv)) {
+    case kGeom128x4: launch_lean_g<Geom<128, 4>>(p, R, batch, grid, s); break;
+    case kGeom128x2: launch_lean_g<Geom<128, 2>>(p, R, batch, grid, s); break;
+    case kGeom128x1: launch_lean_g<Geom<128, 1>>(p, R, batch, grid, s); break;
+    case kGeom64x4: launch_lean_g<Geom<64, 4>>(p, R, batch, grid, s); break;
+    case kGeom64x2: launch_lean_g<Geom<64, 2>>(p, R, batch, grid, s); break;
+    default: break;
+  }
+}
+static int lean_heads_per_group(int head_dim, int n_kv) {
+  switch (lean_geom(head_dim, n_kv)) {
+    case kGeom128x4: case kGeom64x4: return 4;
+    case kGeom128x2: case kGeom64x2: return 2;
+    default: return 1;
   }
 }
 
-// Same counter region | partial O / l [2 grid, n_kv, R, head_dim] fp16 | log-sum-exp
-// [2 grid, n_kv, R] fp32.
+// Same counter region | partial O / l [2 grid, HG, R, head_dim] fp16 | log-sum-exp
+// [2 grid, HG, R] fp32, sized for the widest geometry (4 heads of head_dim 128 per slot).
 constexpr size_t kLeanRowBytes = rows::HD * 2 + sizeof(float);
 static size_t ws_bytes_lean(int grid, int R) {
   return kCounterBytes + size_t(2) * grid * rows::NKV * R * kLeanRowBytes;
@@ -2537,6 +2702,7 @@ static void fill_params(AttnParams& p, const void* q, int64_t q_sb, int64_t q_ss
   p.cascade_splits = 0;
   p.n_groups = 1;
   p.tok_elems = 0;  // set by the balanced-kernel launches
+  p.cnt_stride = 1;
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
 }
 
@@ -2722,13 +2888,16 @@ static int decode_attn(const char* fn, bool use_scratch, const void* q, int64_t 
     p.ws_cnt = static_cast<int32_t*>(workspace);
     p.ws_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
     p.ws_ml = lean_lse_base(p.ws_o, size_t(2) * grid, R);
-    p.two_pass = merge == PKV_DECODE_FUSED_MERGE ? 0 : 1;
+    // in-launch merge only for decode rows (R <= 16): verify's row count would need too many
+    // merge workgroups, so it always merges in a second launch
+    p.two_pass = merge == PKV_DECODE_FUSED_MERGE && R <= 16 ? 0 : 1;
+    // the counters 128 bytes apart where the counter region has room
+    p.cnt_stride = 1;
+    while (p.cnt_stride < 32 && int64_t(batch) * n_kv * p.cnt_stride * 2 <= kMaxCounters) p.cnt_stride *= 2;
     p.lean_grid = grid;
-    p.n_groups = n_kv / rows::NKV;
+    p.n_groups = n_kv / lean_heads_per_group(head_dim, n_kv);
     p.tok_elems = n_kv * head_dim;
-    launch_lean(p, R, batch, grid, s);
-    if (p.two_pass)
-      combine_lean_kernel<<<dim3(n_kv, batch, (R + 15) / 16), 64 * (R < 16 ? R : 16), 0, s>>>(p, grid);
+    launch_lean(p, head_dim, R, batch, grid, s);
     return check_launch(fn);
   }
 
@@ -2793,7 +2962,8 @@ namespace pkv {
 
 static bool cascade_eligible(int batch, int head_dim, int n_kv, int R, int page_size, int max_blocks,
                              int shared_tokens) {
-  return n_kv == rows::NKV && use_lean_kernel(batch, head_dim, n_kv, R, page_size, 0, 0) && shared_tokens > 0 &&
+  return n_kv == rows::NKV && head_dim == rows::HD && use_lean_kernel(batch, head_dim, n_kv, R, page_size, 0, 0) &&
+         shared_tokens > 0 &&
          shared_tokens % page_size == 0 && int64_t(shared_tokens) <= int64_t(max_blocks) * page_size;
 }
 
@@ -2880,8 +3050,7 @@ extern "C" int pkv_cascade_attn(const void* q, int64_t q_sb, int64_t q_ss, int64
   constexpr int NT = PKV_PREFILL_LDS_NT, W = PKV_PREFILL_LDS_W;
   const dim3 pgrid((batch * R + 16 * NT * W - 1) / (16 * NT * W), rows::NKV, S);
   prefill_lds_kernel<NT, W, PKV_PREFILL_LDS_NBUF, PKV_PREFILL_LDS_SUB, true><<<pgrid, 64 * W, 0, s>>>(p);
-  launch_lean(p, R, batch, grid, s);
-  combine_lean_kernel<<<dim3(rows::NKV, batch, (R + 15) / 16), 64 * (R < 16 ? R : 16), 0, s>>>(p, grid);
+  launch_lean_g<Geom7B>(p, R, batch, grid, s);  // suffix pass + the merge of every part (two_pass)
   return check_launch(fn);
 }
 

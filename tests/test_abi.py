@@ -33,7 +33,7 @@ def test_library_exports_every_header_function(lib):
 def test_header_constants_match_binding(lib):
     defines = dict(re.findall(r"^#define (PKV_\w+) \(?(-?\d+)\)?", HEADER, re.M))
     for name in ["PKV_OK", "PKV_EINVAL", "PKV_EHIP", "PKV_ENOSPC", "PKV_STATUS_BAD_PAGE", "PKV_STATUS_BAD_POSITION",
-                 "PKV_STATUS_SHARED_PREFIX", "PKV_STATUS_PARTIAL_RANGE", "PKV_DECODE_TWO_PASS",
+                 "PKV_STATUS_SHARED_PREFIX", "PKV_STATUS_PARTIAL_RANGE", "PKV_STATUS_MERGE_TIMEOUT", "PKV_DECODE_TWO_PASS",
                  "PKV_DECODE_FUSED_MERGE", "PKV_DECODE_HEADS"]:
         assert int(defines[name]) == getattr(_lib, name), name
     assert int(defines["PKV_ABI_VERSION"]) == _lib.ABI_VERSION == lib.pkv_abi_version()
@@ -92,15 +92,23 @@ def test_decode_workspace_too_small_is_enospc(lib):
 
 
 def test_workspace_bytes_arithmetic(lib):
-    # head_dim 64 never takes the balanced kernel, so this is pure arithmetic: counters (64 KiB)
-    # + batch * n_kv * splits * R * (head_dim + 2) floats
+    # head_dim 64 with an odd n_kv never takes the balanced kernel (nor does a fixed split_tokens),
+    # so this is pure arithmetic: counters (64 KiB) + batch * n_kv * splits * R * (head_dim + 2)
+    # floats
     f = lib.pkv_decode_workspace_bytes
-    assert f(0, 1, 14, 2, 64, 256, 4, 0) == 0
-    assert f(2, 1, 14, 2, 64, 256, 2, 0) == 0          # 512 keys fit the default 512-key split
+    assert f(0, 1, 14, 1, 64, 256, 4, 0) == 0
+    assert f(2, 1, 14, 1, 64, 256, 2, 0) == 0          # 512 keys fit the default 512-key split
     B, s_q, nh, nkv, hd, P, mb, st = 3, 1, 14, 2, 64, 256, 8, 256
     R = s_q * nh // nkv
     splits = -(-(mb * P) // st)
     assert f(B, s_q, nh, nkv, hd, P, mb, st) == 65536 + B * nkv * splits * R * (hd + 2) * 4
+    # the balanced kernel's bound (one workgroup per CU; 256 without a GPU): counters + 2 slots per
+    # workgroup of 4 heads x R rows x (256 B of fp16 + a 4-byte log-sum-exp), for every geometry
+    # it serves, or the per-head kernel's need where that is larger
+    for nh, nkv, hd in [(28, 4, 128), (7, 1, 128), (14, 2, 128), (14, 2, 64), (28, 4, 64), (40, 8, 128)]:
+        R = nh // nkv
+        per_head = 65536 + 2 * nkv * 4 * R * (hd + 2) * 4  # batch 2, 4 splits of 512 keys
+        assert f(2, 1, nh, nkv, hd, 256, 8, 0) == max(65536 + 2 * 256 * 4 * R * 260, per_head)
 
 
 def test_copy_and_gather_argument_errors(lib):

@@ -137,6 +137,45 @@ def test_balanced_kernel_head_groups(gpu, case, merge):
                    grid=grid, two_pass=merge == "two-pass", seed=len(ctx) + grid, what=f"groups{case}-{merge}")
 
 
+# The balanced kernel's narrower geometries: 2 or 1 KV heads of head_dim 128 per group (64- and
+# 128-token tiles, 2 or 4 phase waves per head whose softmax states merge through LDS), head_dim 64
+# in groups of 4 or 2 (two 32-key subtiles per wave; 64- and 128-token tiles): Qwen2.5-0.5B, 7B on
+# 4 and 2 tensor-parallel ranks, 3 and 6 KV heads (several groups), verify row counts whose phase
+# merge needs two rounds (R = 35 with 1 KV head, R = 64 with 2), pages exactly one tile long.
+GEOM_CASES = [
+    # (batch, ctx, page, n_kv, n_heads, hd, s_q, grid, append)
+    (6, [3000, 17, 4100, 800, 1, 2500], 256, 2, 14, 64, 1, 0, True),      # 0.5B
+    (6, [3000, 17, 4100, 800, 1, 2500], 256, 2, 14, 64, 1, 7, True),
+    (6, [3000, 17, 4100, 800, 1, 2500], 256, 1, 7, 128, 1, 0, True),      # 7B, TP 4
+    (6, [3000, 17, 4100, 800, 1, 2500], 256, 1, 7, 128, 1, 5, True),
+    (6, [3000, 17, 4100, 800, 1, 2500], 256, 2, 14, 128, 1, 9, True),     # 7B, TP 2
+    (40, [(i * 37) % 300 for i in range(40)], 128, 1, 7, 128, 1, 5, True),
+    (40, [(i * 37) % 300 for i in range(40)], 64, 2, 14, 128, 1, 3, True),
+    (40, [(i * 37) % 300 for i in range(40)], 128, 2, 14, 64, 1, 11, True),
+    (5, [10, 2000, 130, 40, 250], 128, 3, 21, 128, 1, 3, True),           # 3 groups of 1
+    (5, [10, 2000, 130, 40, 250], 64, 6, 24, 128, 2, 4, True),            # 3 groups of 2
+    (5, [10, 2000, 130, 40, 250], 64, 4, 16, 64, 1, 2, True),             # hd 64, one group of 4
+    (5, [10, 2000, 130, 40, 250], 128, 6, 18, 64, 3, 6, True),            # hd 64, 3 groups of 2
+    (3, [517, 2, 90], 256, 1, 7, 128, 5, 0, True),                        # verify R = 35
+    (3, [517, 2, 90], 256, 1, 7, 128, 5, 4, True),
+    (4, [700, 33, 1, 2000], 256, 1, 7, 128, 9, 6, True),                  # R = 63, appends straddle tiles
+    (2, [61, 700], 256, 2, 16, 128, 8, 3, True),                          # R = 64
+    (2, [61, 700], 256, 2, 16, 64, 8, 3, False),                          # hd 64, R = 64, no append
+    (4, [0, 5, 300, 33], 256, 1, 7, 128, 1, 2, False),
+    (1, [0], 256, 2, 14, 64, 1, 1, True),                                 # empty cache
+    (64, [2027 + (i * 97) % 1024 for i in range(64)], 256, 1, 7, 128, 5, 0, True),
+]
+
+
+@pytest.mark.parametrize("merge", ["two-pass", "in-launch"])
+@pytest.mark.parametrize("case", GEOM_CASES, ids=[f"x{i}" for i in range(len(GEOM_CASES))])
+def test_balanced_kernel_narrow_geometries(gpu, case, merge):
+    B, ctx, P, n_kv, nh, hd, s_q, grid, append = case
+    _run_and_check(gpu, batch=B, ctx=ctx, page_size=P, n_kv=n_kv, n_heads=nh, head_dim=hd, s_q=s_q,
+                   append=append, grid=grid, two_pass=merge == "two-pass", seed=len(ctx) + grid + n_kv,
+                   what=f"geom{case[:1] + case[2:]}-{merge}")
+
+
 def test_balanced_in_launch_merge_rearms_across_calls(gpu):
     # the balanced kernel's per-(sequence, head) arrival counters must be back at zero after every
     # call: consecutive calls of different shapes and grids share one workspace, with sequences
