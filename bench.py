@@ -52,6 +52,7 @@ def parse():
     ap.add_argument("--workload", choices=["config2", "config3", "config4", "config5", "decode-14B", "decode-0.5B",
                                            "decode-7B-tp4", "epilogue", "tables", "peak"], default="config3")
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = library choice)")
+    ap.add_argument("--grid", type=int, default=0, help="workgroups of the balanced kernel (0 = one per CU)")
     ap.add_argument("--layers", type=int, default=0, help="layers (0 = the model's)")
     ap.add_argument("--merge", choices=["auto", "two-pass", "fused"], default="auto",
                     help="split-K merge of the per-head kernel: library choice, second launch, in-launch")
@@ -65,7 +66,8 @@ def parse():
 def profiled_traffic(args, w):
     """HBM bytes per call from the committed FETCH_SIZE / WRITE_SIZE counter passes over this same
     workload (default seed, 28 layers, library-chosen kernel); None for any other configuration."""
-    if (args.workload != "config3" or args.seed != 0 or w.layers != 28 or args.split or args.merge != "auto"
+    if (args.workload != "config3" or args.seed != 0 or w.layers != 28 or args.split or args.grid
+            or args.merge != "auto"
             or not TRAFFIC_PROFILE.exists()):
         return None, None
     for line in TRAFFIC_PROFILE.read_text().splitlines():
@@ -630,7 +632,7 @@ def main() -> int:
         for l in range(L):
             prism_amd.flash_attn_with_kvcache(w.q[l], kv.k_caches[l], kv.v_caches[l], k=w.k[l], v=w.v[l],
                                               cache_seqlens=w.cache_seqlens, block_table=w.block_table,
-                                              causal=True, out=outs[l], split_tokens=args.split,
+                                              causal=True, out=outs[l], split_tokens=args.split, grid=args.grid,
                                               two_pass=two_pass)
 
     step_ms = time_graph(step, args, dev)
@@ -663,7 +665,7 @@ def main() -> int:
     cfg = {"workload": "", "batch": w.batch, "layers": L, "n_heads": w.n_heads, "n_kv": kv.num_kv_heads,
            "head_dim": kv.head_dim, "page_size": kv.page_size, "pool_pages": kv.max_pages, "s_q": w.s_q,
            "sum_ctx": int(w.ctx.sum()), "max_ctx": int(w.ctx.max()), "seed": args.seed,
-           "split_tokens": args.split or "auto", "merge": args.merge}
+           "split_tokens": args.split or "auto", "grid": args.grid or "auto", "merge": args.merge}
     per_call = f"HIP events around K graph replays of the {L}-call step, per call = step / {L}"
     if args.workload in ("config2", "config3") or args.workload.startswith("decode-"):
         traffic, traffic_src = profiled_traffic(args, w)

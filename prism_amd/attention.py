@@ -305,6 +305,8 @@ def flash_attn_with_kvcache(
             return out
         nbytes = lib.pkv_decode_workspace_bytes(batch, s_q, n_heads, n_kv, hd, page_size, max_blocks,
                                                 int(split_tokens))
+        if grid:  # the balanced kernel's partials for `grid` workgroups (prism_kv.h's bound)
+            nbytes = max(nbytes, 65536 + 2 * int(grid) * 4 * s_q * g * 260)
         ws = None if noalloc else _workspace(device, nbytes, stream, allow_static=True)
         if noalloc or (ws is None and nbytes > 0):
             rc = lib.pkv_decode_attn_noalloc(

@@ -1426,8 +1426,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // Log-sum-exp merge of query rows rr[0 .. NR) of (sequence b, KV head hk; rr[q] < 0: none) over
 // n_parts split-K partials (part u of row r at workspace row row_of(u, r)) into the bf16 output,
-// by one wave.  The merge is
-// latency-bound, so everything one round trip can fetch is fetched at once, for up to 64 parts:
+// by one wave.  The merge is latency-bound, so everything one round trip can fetch is fetched at
+// once, for up to BIG parts:
 // lane u loads part u's log-sum-exp, and lane (g, c) = (lane / CPR, lane % CPR) loads the 16 bytes
 // of head-dim chunk c (elements 8c .. 8c + 7; CPR = head_dim / 8 chunks per row) of parts g,
 // g + PG, g + 2 PG, ... of the row (PG = 64 / CPR part groups; 16 or 8 loads in flight per lane:
@@ -1436,9 +1436,10 @@ __device__ __forceinline__ float wave_sum(float v) {
 // No LDS, no barrier; loops stay rolled where the code would otherwise grow (every launch starts
 // from a cold instruction cache).  COH: device-coherent loads (partials written during this
 // launch, by workgroups on any XCD).
-constexpr int kLeanMergeParts = 64;
-
-template <typename G, bool COH, int NR, typename RowOf>
+// BIG: parts per round trip beyond the first 8 (64: up to 16 loads in flight per lane; the
+// combine launch takes 32, for a register count at which several of its workgroups share a CU:
+// config-5 verify's combine 9.9 -> 7.9 us, its cascade merge 13.5 -> 9.2 us).
+template <typename G, bool COH, int NR, int BIG, typename RowOf>
 __device__ __forceinline__ void merge_rows(const AttnParams& p, int hk, int b, const int (&rr)[NR], int n_parts,
                                            RowOf row_of) {
   constexpr int HD = G::HD;
@@ -1513,8 +1514,8 @@ __device__ __forceinline__ void merge_rows(const AttnParams& p, int hk, int b, c
     batch(std::integral_constant<int, 8 / PG>(), 0, n_parts);
   } else {
 #pragma unroll 1
-    for (int u0 = 0; u0 < n_parts; u0 += kLeanMergeParts)
-      batch(std::integral_constant<int, kLeanMergeParts / PG>(), u0, min(kLeanMergeParts, n_parts - u0));
+    for (int u0 = 0; u0 < n_parts; u0 += BIG)
+      batch(std::integral_constant<int, BIG / PG>(), u0, min(BIG, n_parts - u0));
   }
 #pragma unroll
   for (int q = 0; q < NR; ++q) {
@@ -1581,7 +1582,7 @@ __device__ __forceinline__ void merge_workgroup(const AttnParams& p, const SeqTa
   const int r0 = 4 * rq + int(threadIdx.x >> 6);
   const int rr[1] = {r0 < p.R ? r0 : -1};
   if (ready && rr[0] >= 0)
-    merge_rows<G, true, 1>(p, hk, b, rr, sp.np, [&](int part, int r) -> int64_t {
+    merge_rows<G, true, 1, 64>(p, hk, b, rr, sp.np, [&](int part, int r) -> int64_t {
       const int slot = part == 0 ? sp.slot0 : 2 * (sp.w0 + part);
       return (int64_t(slot) * G::HG + h) * p.R + r;
     });
@@ -1732,10 +1733,11 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     raw_barrier();  // ... and every other wave's
     if (j == 0 || d.T0 == p.k0) {
       // a segment starts: its Q operand, row limits and a fresh softmax state
-      if constexpr (kQInLds)
+      if constexpr (kQInLds) {
         rows_read_q<G>(p, buf, hg, qf);
-      else
+      } else {
         rows_load_q<HD, NT>(p, d, d.g * G::HG + hg, qf);
+      }
       seg_j0 = j;
       seg_T0 = d.T0;
       lim_min = 0x7fffffff;
@@ -1900,16 +1902,17 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
 }
 
 // Two-pass merge (PKV_DECODE_TWO_PASS) of the partials a decode_lean_kernel launch of `grid`
-// workgroups left in the workspace.  Workgroup (KV head, sequence, group of 16 query rows), one
-// wave per query row (merge_row); only sequences whose tiles span more than one range have
+// workgroups left in the workspace.  Workgroup (KV head, sequence, group of 8 query rows), one
+// wave per query row (merge_rows; 8-wave workgroups pack three to a CU at its register count,
+// where 16-wave ones ran one at a time); only sequences whose tiles span more than one range have
 // partials, and in a cascade launch every sequence has the prefix pass's parts as well.
 template <typename G>
-__global__ __launch_bounds__(1024) void combine_lean_kernel(const AttnParams p, int grid) {
+__global__ __launch_bounds__(512) void combine_lean_kernel(const AttnParams p, int grid) {
   const int hk = blockIdx.x;  // KV head; its group's tiles follow those of the groups before it
   const int g = hk / G::HG;
   const int h = hk - g * G::HG;  // head within the group (the partials hold HG per slot)
   const int b = blockIdx.y;
-  const int r = int(blockIdx.z) * 16 + int(threadIdx.x >> 6);  // query row of this wave
+  const int r = int(blockIdx.z) * 8 + int(threadIdx.x >> 6);  // query row of this wave
   const int lane = threadIdx.x & 63;
   if (r >= p.R) return;
 
@@ -1946,7 +1949,7 @@ __global__ __launch_bounds__(1024) void combine_lean_kernel(const AttnParams p, 
   // the first range holds b in its first segment only if b starts exactly at the range start
   const int slot0 = 2 * w0 + (first != w0 * per ? 1 : 0);
   const int rr[1] = {r};
-  merge_rows<G, false, 1>(p, hk, b, rr, n_parts, [&](int part, int r) -> int64_t {
+  merge_rows<G, false, 1, 32>(p, hk, b, rr, n_parts, [&](int part, int r) -> int64_t {
     int slot;
     if (part < S) {
       slot = 2 * grid + b * S + part;
@@ -2603,7 +2606,7 @@ static void launch_lean_g(const AttnParams& p, int R, int batch, int grid, hipSt
     }
   }
   if (p.two_pass)
-    combine_lean_kernel<G><<<dim3(p.n_kv, batch, (R + 15) / 16), 64 * (R < 16 ? R : 16), 0, s>>>(p, grid);
+    combine_lean_kernel<G><<<dim3(p.n_kv, batch, (R + 7) / 8), 64 * (R < 8 ? R : 8), 0, s>>>(p, grid);
 }
 static void launch_lean(const AttnParams& p, int head_dim, int R, int batch, int grid, hipStream_t s) {
   switch (lean_geom(head_dim, p.n_kv)) {
