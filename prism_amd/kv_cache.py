@@ -40,6 +40,17 @@ from . import _lib
 from .attention import status_tensor
 
 
+def shared_prefix_pages(bt_host: np.ndarray, sl_host: np.ndarray, page_size: int) -> int:
+    """Leading block-table columns that every row of a batch of two or more lists the same page
+    in, counting only pages that every sequence fills (sl >= (c + 1) * page_size): the prefix
+    cascade attention may read once for the batch (branches of one prompt, prefix-cache hits)."""
+    if bt_host.shape[0] < 2 or bt_host.shape[1] == 0:
+        return 0
+    same = (bt_host == bt_host[0:1]).all(axis=0) & (bt_host[0] >= 0)
+    k = int(same.argmin()) if not same.all() else int(same.size)
+    return min(k, int(sl_host.min()) // page_size)
+
+
 class KVCacheOutOfPages(RuntimeError, IndexError):
     """No free KV page left (is-a RuntimeError and an IndexError, matching both reference paths)."""
 
@@ -284,6 +295,11 @@ class FlashAttnKVCache:
         staged_sl.numpy()[:] = sl_host
         bt.copy_(staged_bt, non_blocking=pin)
         sl.copy_(staged_sl, non_blocking=pin)
+        # the keys every sequence of the batch shares (identical leading pages, filled by all):
+        # recorded with both tensors' version counters, so that flash_attn_with_kvcache can take
+        # cascade attention for this table as long as neither has been written since
+        shared = shared_prefix_pages(bt_host, sl_host, self.page_size) * self.page_size
+        bt._pkv_shared_prefix = (shared, bt._version, sl.data_ptr(), sl._version)
         return bt, sl
 
     # ------------------------------------------------------------------ page movement

@@ -129,3 +129,48 @@ def test_cascade_without_append_checks_row_visibility(gpu):
                                       block_table=dev["block_table"], causal=True, shared_prefix_tokens=shared)
     torch.cuda.synchronize()
     assert prism_amd.read_status(gpu) & prism_amd._lib.PKV_STATUS_SHARED_PREFIX
+
+
+def test_cascade_chosen_from_the_block_table_of_forked_branches(gpu):
+    # a verify batch of 8 branches forked from one 2000-token prompt, each grown by its own suffix
+    # (the boundary page copied on write): build_block_table records the 7 shared full pages and
+    # flash_attn_with_kvcache, called exactly as the reference calls it (no shared-prefix
+    # argument), takes cascade attention; results match the oracle and the ordinary path
+    from prism_amd import shared_prefix_of
+    P, n_kv, hd, nh, s_q = 256, 4, 128, 28, 5
+    kv = prism_amd.FlashAttnKVCache(1, n_kv, hd, 64, P, str(gpu))
+    g = torch.Generator().manual_seed(7)
+    kv.k_pool.copy_(torch.randn(kv.k_pool.shape, generator=g).to(torch.bfloat16))
+    kv.v_pool.copy_(torch.randn(kv.v_pool.shape, generator=g).to(torch.bfloat16))
+    kv.new_sequence(0)
+    kv._ensure_capacity(0, 2000)
+    kv.seq_len[0] = 2000
+    ids = list(range(8))
+    for sid in ids[1:]:
+        kv.fork_sequence(0, sid)
+    for sid in ids:
+        grow = (sid * 37) % 300
+        kv.prepare_append([sid], grow)
+        kv.update_seqlens([sid], grow)
+    kv.prepare_append(ids, s_q)
+    bt, sl = kv.build_block_table(ids)
+    assert shared_prefix_of(bt, sl) == 7 * P
+    q = torch.randn(len(ids), s_q, nh, hd, generator=g).to(torch.bfloat16)
+    k = torch.randn(len(ids), s_q, n_kv, hd, generator=g).to(torch.bfloat16)
+    v = torch.randn(len(ids), s_q, n_kv, hd, generator=g).to(torch.bfloat16)
+    kc_cpu, vc_cpu = kv.k_caches[0].cpu(), kv.v_caches[0].cpu()
+    kc0, vc0 = kv.k_caches[0].clone(), kv.v_caches[0].clone()
+    print(f"auto cascade B={len(ids)} shared={7 * P} s_q={s_q}", flush=True)
+    out = prism_amd.flash_attn_with_kvcache(q.to(gpu), kv.k_caches[0], kv.v_caches[0], k.to(gpu), v.to(gpu),
+                                            cache_seqlens=sl, block_table=bt, causal=True)
+    torch.cuda.synchronize()
+    assert prism_amd.read_status(gpu) == 0
+    ref, kb, vb = pa.flash_attn_with_kvcache_ref(q, kc_cpu, vc_cpu, k, v, cache_seqlens=sl.cpu(),
+                                                 block_table=bt.cpu(), causal=True)
+    assert np.array_equal(pa.bf16_bits(kv.k_caches[0]), kb), "K cache not bit-exact after append"
+    assert np.array_equal(pa.bf16_bits(kv.v_caches[0]), vb), "V cache not bit-exact after append"
+    assert_attn_close(out, ref, "auto cascade")
+    plain = prism_amd.flash_attn_with_kvcache(q.to(gpu), kc0, vc0, k.to(gpu), v.to(gpu), cache_seqlens=sl,
+                                              block_table=bt, causal=True, shared_prefix_tokens=0)
+    torch.cuda.synchronize()
+    assert float((plain.float() - out.float()).abs().max()) <= 1.6e-2

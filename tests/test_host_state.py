@@ -246,3 +246,44 @@ def test_unassigned_block_table_columns_never_name_a_live_page():
     page_of = slots // 16
     assert page_of[0, 0] in kv.seq_pages[0]
     assert page_of[1, 0] < 0 and page_of[1, 0] not in live   # the kernels flag it and skip the write
+
+
+def test_build_block_table_records_the_shared_prefix(copies):
+    # branches of one prompt (forks of a 40-token sequence on 16-token pages): two full pages are
+    # shared and filled by every branch; the third column is shared too but not full, and after
+    # copy-on-write each branch holds its own copy of it
+    from prism_amd import shared_prefix_of
+    from prism_amd.kv_cache import shared_prefix_pages
+    kv = _kv(pages=24, P=16)
+    kv.new_sequence(0)
+    kv._ensure_capacity(0, 40)
+    kv.seq_len[0] = 40
+    for sid in (1, 2, 3):
+        kv.fork_sequence(0, sid)
+    bt, sl = kv.build_block_table([0, 1, 2, 3])
+    assert shared_prefix_of(bt, sl) == 32
+    kv.prepare_append([0, 1, 2, 3], 5)
+    bt, sl = kv.build_block_table([0, 1, 2, 3])
+    assert len(set(bt[:, 2].tolist())) == 4 and shared_prefix_of(bt, sl) == 32
+    # stale or foreign tensors record nothing
+    assert shared_prefix_of(bt.clone(), sl) == 0
+    assert shared_prefix_of(bt, sl.clone()) == 0
+    bt2, sl2 = kv.build_block_table([0, 1, 2, 3])   # rebuilt into the same buffers: bt is stale
+    assert shared_prefix_of(bt, sl) == 0 and shared_prefix_of(bt2, sl2) == 32
+    bt2[1, 0] = bt2[1, 0]                              # any in-place write drops it
+    assert shared_prefix_of(bt2, sl2) == 0
+    # one sequence, or a batch that shares nothing, has no shared prefix
+    bt, sl = kv.build_block_table([0])
+    assert shared_prefix_of(bt, sl) == 0
+    kv.new_sequence(9)
+    kv._ensure_capacity(9, 40)
+    kv.seq_len[9] = 40
+    bt, sl = kv.build_block_table([0, 9])
+    assert shared_prefix_of(bt, sl) == 0
+    # the count itself: identical leading columns, capped by the shortest sequence's full pages
+    t = np.array([[3, 4, 5, 6], [3, 4, 5, 7], [3, 4, 5, -1]], dtype=np.int32)
+    assert shared_prefix_pages(t, np.array([64, 64, 48]), 16) == 3
+    assert shared_prefix_pages(t, np.array([64, 64, 47]), 16) == 2
+    assert shared_prefix_pages(t[:1], np.array([64]), 16) == 0
+    assert shared_prefix_pages(np.full((2, 3), -1, dtype=np.int32), np.array([0, 0]), 16) == 0
+    _check_invariants(kv)
