@@ -15,7 +15,8 @@ bytes per step / step time (GB/s), the per-call roofline (step time / layers) an
 (the oracle's torch-CPU reference path on a bounded sample of the same workload, N=1 only).
 
 --workload config2 / config4 / config5 measures the other configurations the same way (decode at
-b=8 ctx 2048; 14B chunked prefill, MFMA-bound, in TFLOP/s; 7B shared-prefix speculative verify,
+b=8 ctx 2048; 14B chunked prefill, MFMA-bound, in TFLOP/s; 7B shared-prefix speculative verify in
+GB/s of unique KV bytes, the shared prefix counted once, on the ordinary and the cascade path,
 plus its copy-on-write and a compaction of every live page into a fresh pool).  --workload
 epilogue times the elementwise kernels on either side of attention (QKV split + RoPE + paged
 append, RMSNorm with the residual add, SiLU-mul) at the 14B prefill-chunk and 7B decode scales.
@@ -41,6 +42,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_PROFILE = ROOT / "profiles" / "decode_config3_traffic.md"
+VERIFY_TRAFFIC_PROFILE = ROOT / "profiles" / "verify_config5_traffic.md"
 
 
 def parse():
@@ -63,16 +65,16 @@ def parse():
     return ap.parse_args()
 
 
-def profiled_traffic(args, w):
+def profiled_traffic(args, w, key="traffic_bytes_per_call"):
     """HBM bytes per call from the committed FETCH_SIZE / WRITE_SIZE counter passes over this same
-    workload (default seed, 28 layers, library-chosen kernel); None for any other configuration."""
-    if (args.workload != "config3" or args.seed != 0 or w.layers != 28 or args.split or args.grid
-            or args.merge != "auto"
-            or not TRAFFIC_PROFILE.exists()):
+    workload (config 3 or 5, default seed, 28 layers, library-chosen kernel); None otherwise."""
+    profile = {"config3": TRAFFIC_PROFILE, "config5": VERIFY_TRAFFIC_PROFILE}.get(args.workload)
+    if (profile is None or args.seed != 0 or w.layers != 28 or args.split or args.grid or args.merge != "auto"
+            or not profile.exists()):
         return None, None
-    for line in TRAFFIC_PROFILE.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_call:"):
-            return int(line.split(":", 1)[1]), str(TRAFFIC_PROFILE.relative_to(ROOT))
+    for line in profile.read_text().splitlines():
+        if line.startswith(key + ":"):
+            return int(line.split(":", 1)[1]), str(profile.relative_to(ROOT))
     return None, None
 
 
@@ -764,18 +766,26 @@ def main() -> int:
         del wl, outs_l
         torch.cuda.empty_cache()
         page_ops = config5_page_ops(prism_amd, w, dev)
+        # the HBM roofline counts every key once (the shared prefix once for the batch): the
+        # per-sequence re-reads of the prefix are served by the caches, so they are reported apart
+        gbs_unique = unique_layer / (call_us * 1e-6) / 1e9
+        traffic, traffic_src = profiled_traffic(args, w)
+        cascade["traffic"], _ = profiled_traffic(args, w, "cascade_traffic_bytes_per_call")
         result = {
-            "metric": "speculative verify attn HBM GB/s (% of peak) + MFMA %, Qwen2.5-7B shape b=64 draft 5",
-            "value": round(bytes_layer * L / (step_ms * 1e-3) / 1e9, 2), "unit": "GB/s", **common,
+            "metric": "speculative verify attn GB/s of unique KV bytes (% of HBM peak) + MFMA %, "
+                      "Qwen2.5-7B shape b=64 draft 5",
+            "value": round(unique_layer * L / (step_ms * 1e-3) / 1e9, 2), "unit": "GB/s", **common,
             "config": cfg,
             "roofline": {
-                "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "bound": "hbm", "achieved": round(gbs_unique, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs_unique / HBM_PEAK_GBS, 4), "traffic": traffic,
+                **({"traffic_source": traffic_src} if traffic_src else {}),
                 "mfma_tflops": round(tflops, 2), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                 "kernel": "one pkv_decode_attn call (s_q=5, 35 query rows per KV head) = decode_lean_kernel<3> "
                           "(balanced tile ranges, 3 MFMA row tiles per wave) + combine_lean_kernel; bytes count "
-                          "every sequence's reads of the shared prefix; " + per_call,
-                "bytes_per_call": bytes_layer, "flops_per_call": flops_layer, "avg_call_us": round(call_us, 3),
+                          "every key once, the shared prefix once for the batch; " + per_call,
+                "bytes_per_call": unique_layer, "flops_per_call": flops_layer, "avg_call_us": round(call_us, 3),
+                "per_sequence_bytes_per_call": bytes_layer, "gbs_per_sequence": round(gbs, 1),
             },
             "page_ops": page_ops,
             "cascade": cascade,
