@@ -19,7 +19,9 @@ b=8 ctx 2048; 14B chunked prefill, MFMA-bound, in TFLOP/s; 7B shared-prefix spec
 GB/s of unique KV bytes, the shared prefix counted once, on the ordinary and the cascade path,
 plus its copy-on-write and a compaction of every live page into a fresh pool).  --workload
 epilogue times the elementwise kernels on either side of attention (QKV split + RoPE + paged
-append, RMSNorm with the residual add, SiLU-mul) at the 14B prefill-chunk and 7B decode scales.
+append, RMSNorm with the residual add, SiLU-mul) at the 14B prefill-chunk and 7B decode scales,
+and config 3's decode step from the QKV projection on as two launches (rope_qk, attention) and as
+one (rope_decode_attention).
 --workload tables times the per-step host staging of a graph-captured decode batch (block table,
 lengths, rotary rows) at config 3's batch: DecodeBatch against the reference's refill.
 --workload decode-14B / decode-0.5B / decode-7B-tp4 run config 3's ragged batch at other model
@@ -322,6 +324,56 @@ def epilogue_bench(args, dev) -> dict:
     return res
 
 
+def decode_step_bench(args, dev) -> dict:
+    """Config 3's decode batch from the fused QKV projection on, per layer: rope_qk (split + RoPE
+    + append) followed by attention over cache_seqlens + 1, against rope_decode_attention (the
+    same in one launch), with the plain append + attention call (rotated q / k given) beside them.
+    Each is a graph of the 28-layer step; HIP events around the replays, per layer = step / 28."""
+    import torch
+
+    import prism_amd
+    from prism_amd import workloads
+
+    w = workloads.config3(dev, seed=args.seed)
+    kv, L, B = w.kv, w.layers, w.batch
+    nh, nkv, hd = w.n_heads, kv.num_kv_heads, kv.head_dim
+    g = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    qkv = [torch.randn(B, 1, (nh + 2 * nkv) * hd, generator=g, device=dev).to(torch.bfloat16) for _ in range(L)]
+    cos, sin = prism_amd.rope_tables(hd, int(w.ctx.max()) + 2, device=dev)
+    sl, sl1, bt = w.cache_seqlens, w.cache_seqlens + 1, w.block_table
+    qbuf = [torch.empty(B, 1, nh, hd, dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    outs = [torch.empty(B, 1, nh, hd, dtype=torch.bfloat16, device=dev) for _ in range(L)]
+
+    def two_launch():
+        for l in range(L):
+            prism_amd.rope_qk(qkv[l], sl, cos, sin, nh, nkv, return_k=False, q_out=qbuf[l],
+                              k_cache=kv.k_caches[l], v_cache=kv.v_caches[l], block_table=bt, cache_seqlens=sl)
+            prism_amd.flash_attn_with_kvcache(qbuf[l], kv.k_caches[l], kv.v_caches[l], cache_seqlens=sl1,
+                                              block_table=bt, causal=True, out=outs[l])
+
+    def fused():
+        for l in range(L):
+            prism_amd.rope_decode_attention(qkv[l], kv.k_caches[l], kv.v_caches[l], cos, sin, cache_seqlens=sl,
+                                            block_table=bt, n_heads=nh, n_kv=nkv, out=outs[l])
+
+    def attention_only():
+        for l in range(L):
+            prism_amd.flash_attn_with_kvcache(w.q[l], kv.k_caches[l], kv.v_caches[l], k=w.k[l], v=w.v[l],
+                                              cache_seqlens=sl, block_table=bt, causal=True, out=outs[l])
+
+    res = {"layers": L, "batch": B}
+    for name, fn in (("rope_qk_then_attention", two_launch), ("rope_decode_attention", fused),
+                     ("append_attention_rotated_inputs", attention_only)):
+        us = time_graph(fn, args, dev) * 1e3 / L
+        res[name + "_us"] = round(us, 2)
+        print(f"[bench] config3 step {name}: {us:.2f} us per layer", file=sys.stderr, flush=True)
+    if prism_amd.read_status(dev):
+        print("[bench] WARNING: kernel status flags set", file=sys.stderr)
+    del w, kv
+    torch.cuda.empty_cache()
+    return res
+
+
 def epilogue_cpu_baseline(seed: int) -> dict:
     """The reference's eager torch expressions on the host cores (engine/executor.py:108-127 with
     the Triton norms restated in torch), on 1/8 of the 14B chunk (512 tokens)."""
@@ -567,6 +619,7 @@ def main() -> int:
                                    "graph replays of 20 calls over 8 per-layer buffer sets",
                          "bytes_per_call": pf[dom]["bytes"], "avg_call_us": pf[dom]["us"]},
             "kernels": res,
+            "decode_step_config3": decode_step_bench(args, dev),
         }
         if not args.no_cpu_baseline:
             result["cpu_baseline"] = epilogue_cpu_baseline(args.seed)

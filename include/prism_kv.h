@@ -168,6 +168,33 @@ int pkv_decode_attn_noalloc(const void* q, int64_t q_sb, int64_t q_ss, int64_t q
                             int32_t* status, void* stream);
 
 /*
+ * pkv_decode_attn with the rotary embedding of the call's new tokens fused in: q and k_new arrive
+ * unrotated (the QKV projection's output, e.g. strided views of one [B, s_q, (n_heads + 2 n_kv)
+ * * head_dim] tensor) and token j of sequence b is rotated with row cache_seqlens[b] + j of
+ * cos_tab / sin_tab ([n_pos, head_dim] bf16, the reference's cat([cos, cos]) tables) exactly as
+ * the reference rotates q and k before its flash_attn call (engine/executor.py:149-153, :258-261:
+ * out = x * cos + rotate_half(x) * sin, each bf16 op rounded), in the attention launch itself:
+ * the appended cache rows are bit-identical to pkv_rope_qk's.  A position outside the table is
+ * clamped and sets PKV_STATUS_BAD_POSITION.  Runs on the balanced decode kernel only (head_dim
+ * 128, or 64 with an even n_kv; page_size a tile or more; batch <= 256) with s_q * n_heads / n_kv
+ * + 2 s_q <= 16 (decode of every Qwen2.5 shape): other shapes fail with PKV_EINVAL.  Same
+ * workspace (pkv_decode_workspace_bytes with split_tokens 0) and flags (PKV_DECODE_HEADS
+ * excepted) as pkv_decode_attn.
+ */
+int pkv_decode_attn_rope(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                         const void* k_new, int64_t kn_sb, int64_t kn_ss, int64_t kn_sh,
+                         const void* v_new, int64_t vn_sb, int64_t vn_ss, int64_t vn_sh,
+                         void* k_cache, void* v_cache, int64_t cache_page_stride,
+                         const int32_t* block_table, int64_t bt_stride, const int32_t* cache_seqlens,
+                         const void* cos_tab, const void* sin_tab, int32_t n_pos,
+                         void* out, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+                         void* workspace, size_t workspace_bytes,
+                         int32_t batch, int32_t s_q, int32_t n_heads, int32_t n_kv, int32_t head_dim,
+                         int32_t page_size, int32_t num_pages, int32_t max_blocks,
+                         int32_t causal, float softmax_scale, int32_t flags,
+                         int32_t* status, void* stream);
+
+/*
  * Cascade (shared-prefix) attention: pkv_decode_attn for a batch whose sequences all list the
  * same pages for their first shared_tokens keys (branches of one prompt: the speculative verify
  * of engine/speculative_executor.py:113-164 over a cached prefix, engine/prefix_cache.py).

@@ -59,6 +59,20 @@ _SIGNATURES = {
         _I32, c_float, _I32, _I32,       # causal, scale, split_tokens, flags
         _P, _P,                          # status, stream
     ]),
+    "pkv_decode_attn_rope": (c_int32, [
+        _P, _I64, _I64, _I64,            # q
+        _P, _I64, _I64, _I64,            # k_new
+        _P, _I64, _I64, _I64,            # v_new
+        _P, _P, _I64,                    # caches
+        _P, _I64, _P,                    # block table, seqlens
+        _P, _P, _I32,                    # cos, sin tables, n_pos
+        _P, _I64, _I64, _I64,            # out
+        _P, c_size_t,                    # workspace
+        _I32, _I32, _I32, _I32, _I32,    # batch, s_q, n_heads, n_kv, head_dim
+        _I32, _I32, _I32,                # page_size, num_pages, max_blocks
+        _I32, c_float, _I32,             # causal, scale, flags
+        _P, _P,                          # status, stream
+    ]),
     "pkv_decode_attn_noalloc": (c_int32, [
         _P, _I64, _I64, _I64,            # q
         _P, _I64, _I64, _I64,            # k_new

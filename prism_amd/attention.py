@@ -386,6 +386,70 @@ def decode_attention(q, k_cache, v_cache, k=None, v=None, *, cache_seqlens, bloc
                                    shared_prefix_tokens=0, out=out, status=status)
 
 
+def rope_decode_attention(qkv: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, cos: torch.Tensor,
+                          sin: torch.Tensor, *, cache_seqlens: torch.Tensor, block_table: torch.Tensor, n_heads: int,
+                          n_kv: int, causal: bool = True, softmax_scale: float | None = None,
+                          two_pass: bool | None = None, grid: int = 0, out: torch.Tensor | None = None,
+                          status: torch.Tensor | None = None) -> torch.Tensor:
+    """The reference's decode attention from the fused QKV projection on, in one launch
+    (pkv_decode_attn_rope): the QKV split of ``qkv`` [B, s_q, (n_heads + 2 n_kv) * hd] by strided
+    views, q and k rotated at positions cache_seqlens[b] + j with rows of ``cos`` / ``sin``
+    ([n_pos, hd], rope_tables), the rotated k and v appended at cache_seqlens[b] + j, and paged
+    attention over the cache -- the same values as
+
+        q, k, v = split(qkv); q = q * cos + rotate_half(q) * sin; k = k * cos + rotate_half(k) * sin
+        flash_attn_with_kvcache(q, k_cache, v_cache, k=k, v=v, cache_seqlens=..., block_table=...)
+
+    (engine/executor.py:141-153, :250-261; the appended rows bit-identical to rope_qk's).  Decode
+    shapes only: the balanced kernel with s_q * n_heads / n_kv + 2 s_q <= 16 (every Qwen2.5
+    model's decode step); other shapes raise -- call rope_qk, then flash_attn_with_kvcache."""
+    _require_gpu(qkv, "qkv")
+    num_pages, page_size, kv_heads, hd = _check_cache(k_cache, v_cache)
+    if kv_heads != n_kv:
+        raise RuntimeError(f"n_kv {n_kv} != the cache's {kv_heads} KV heads")
+    if qkv.dtype != _BF16 or qkv.dim() != 3 or qkv.shape[2] != (n_heads + 2 * n_kv) * hd or qkv.stride(2) != 1:
+        raise RuntimeError(f"qkv must be bfloat16 [B, s_q, {(n_heads + 2 * n_kv) * hd}], contiguous in its last dim")
+    if qkv.device != k_cache.device:
+        raise RuntimeError("qkv must be on the cache's device")
+    for name, t in (("cos", cos), ("sin", sin)):
+        if t.dtype != _BF16 or t.dim() != 2 or t.shape[1] != hd or not t.is_contiguous() or t.device != qkv.device:
+            raise RuntimeError(f"{name} must be a contiguous bfloat16 [n_pos, {hd}] table on the qkv device")
+    if cos.shape != sin.shape:
+        raise RuntimeError("cos and sin tables differ in shape")
+    batch, s_q = qkv.shape[0], qkv.shape[1]
+    q = qkv[:, :, :n_heads * hd].unflatten(2, (n_heads, hd))
+    k = qkv[:, :, n_heads * hd:(n_heads + n_kv) * hd].unflatten(2, (n_kv, hd))
+    v = qkv[:, :, (n_heads + n_kv) * hd:].unflatten(2, (n_kv, hd))
+    qs, ks, vs = _rows(q, "q", n_heads, hd), _rows(k, "k", n_kv, hd), _rows(v, "v", n_kv, hd)
+    device = k_cache.device
+    _check_table(block_table, cache_seqlens, batch, device)
+    max_blocks = block_table.shape[1]
+    scale = float(softmax_scale) if softmax_scale is not None else 1.0 / math.sqrt(hd)
+    if out is None:
+        out = torch.empty((batch, s_q, n_heads, hd), dtype=_BF16, device=device)
+    os_ = _rows(out, "out", n_heads, hd)
+    if batch == 0:
+        return out
+    st = status if status is not None else status_tensor(device)
+    lib = _lib.load()
+    stream = _stream_ptr(device)
+    nbytes = lib.pkv_decode_workspace_bytes(batch, s_q, n_heads, n_kv, hd, page_size, max_blocks, 0)
+    if grid:
+        nbytes = max(nbytes, 65536 + 2 * int(grid) * 4 * s_q * (n_heads // n_kv) * 260)
+    ws = _workspace(device, nbytes, stream)
+    rc = lib.pkv_decode_attn_rope(
+        q.data_ptr(), *qs, k.data_ptr(), *ks, v.data_ptr(), *vs,
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
+        block_table.data_ptr(), block_table.stride(0), cache_seqlens.data_ptr(),
+        cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+        out.data_ptr(), *os_,
+        ws.data_ptr() if ws is not None else 0, ws.numel() if ws is not None else 0,
+        batch, s_q, n_heads, n_kv, hd, page_size, num_pages, max_blocks,
+        1 if causal else 0, scale, _decode_flags(two_pass, "auto", grid), st.data_ptr(), stream)
+    _lib.check(rc, "pkv_decode_attn_rope")
+    return out
+
+
 def prefill_attention(q, k_cache, v_cache, k=None, v=None, *, cache_seqlens, block_table,
                       causal=True, softmax_scale=None, out=None, status=None):
     """Force the row-parallel prefill kernel (any s_q)."""

@@ -62,6 +62,12 @@ struct AttnParams {
   // those of group g - 1; tok_elems = n_kv * head_dim, the elements of a token row; cnt_stride:
   // int32 words between the in-launch merge's arrival counters
   int n_groups, tok_elems, cnt_stride;
+  // pkv_decode_attn_rope: q and k_new arrive unrotated; the balanced kernel applies the
+  // reference's rotary embedding (rows positions[b] + j of rot_cos / rot_sin, [n_pos, head_dim])
+  // to both.  Null otherwise.
+  const uint16_t* rot_cos;
+  const uint16_t* rot_sin;
+  int n_pos;
   float scale_log2;  // softmax_scale * log2(e)
 };
 
@@ -1093,6 +1099,53 @@ __device__ __forceinline__ bool tile_has_new(const AttnParams& p, const TileDesc
   return p.has_new && d.T0 + TOK > d.c && d.T0 < d.L;
 }
 
+// Rotary position of a token, clamped into the table (outside it: flagged, PKV_STATUS_BAD_POSITION).
+__device__ __forceinline__ int rope_position(const AttnParams& p, int pos) {
+  if (pos < 0 || pos >= p.n_pos) {
+    if ((threadIdx.x & 63) == 0) flag_status(p.status, PKV_STATUS_BAD_POSITION);
+    pos = min(max(pos, 0), p.n_pos - 1);
+  }
+  return pos;
+}
+
+__device__ __forceinline__ float bf16r(float x) { return bf16_bits_to_f32(f32_to_bf16_bits(x)); }
+__device__ __forceinline__ void unpack_bf16x8(const u32x4 v, float (&f)[8]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    f[2 * k] = bf16_bits_to_f32(v[k] & 0xffffu);
+    f[2 * k + 1] = bf16_bits_to_f32(v[k] >> 16);
+  }
+}
+// The reference's rotary step on one 8-element chunk pair, x1 = elements d .. d+7 (first half of
+// the head) and x2 = d + hd/2 .. (its rotate_half partner): out = x * cos + rotate_half(x) * sin
+// with rotate_half(x) = (-x2, x1), every torch bf16 op rounded (engine/executor.py:149-150):
+// o1 = bf16(bf16(x1 c1) + bf16(-x2 s1)), o2 = bf16(bf16(x2 c2) + bf16(x1 s2)).
+__device__ __forceinline__ void rope_pair(u32x4& a, u32x4& b, const u32x4 c1v, const u32x4 s1v, const u32x4 c2v,
+                                          const u32x4 s2v) {
+  float x1[8], x2[8], c1[8], s1[8], c2[8], s2[8];
+  unpack_bf16x8(a, x1);
+  unpack_bf16x8(b, x2);
+  unpack_bf16x8(c1v, c1);
+  unpack_bf16x8(s1v, s1);
+  unpack_bf16x8(c2v, c2);
+  unpack_bf16x8(s2v, s2);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    a[k] = pack_bf16x2(bf16r(bf16r(x1[2 * k] * c1[2 * k]) + bf16r(-x2[2 * k] * s1[2 * k])),
+                       bf16r(bf16r(x1[2 * k + 1] * c1[2 * k + 1]) + bf16r(-x2[2 * k + 1] * s1[2 * k + 1])));
+    b[k] = pack_bf16x2(bf16r(bf16r(x2[2 * k] * c2[2 * k]) + bf16r(x1[2 * k] * s2[2 * k])),
+                       bf16r(bf16r(x2[2 * k + 1] * c2[2 * k + 1]) + bf16r(x1[2 * k + 1] * s2[2 * k + 1])));
+  }
+}
+// rope_pair on one word (two elements) of x1 and of its partner x2.
+__device__ __forceinline__ void rope_word(uint32_t& a, uint32_t& b, uint32_t c1, uint32_t s1, uint32_t c2,
+                                          uint32_t s2) {
+  u32x4 va = {a, 0u, 0u, 0u}, vb = {b, 0u, 0u, 0u};
+  rope_pair(va, vb, u32x4{c1, 0u, 0u, 0u}, u32x4{s1, 0u, 0u, 0u}, u32x4{c2, 0u, 0u, 0u}, u32x4{s2, 0u, 0u, 0u});
+  a = va[0];
+  b = vb[0];
+}
+
 // Where lane l's 16 bytes of LDS row r of a tile come from: LDS chunk l holds chunk
 // v = (l & 15) ^ swz(r) of wave slice w = l / 16 (head hg = w % HG, phase ph = w / HG): chunk
 // v % SCH of head hg's row of token 32 (S ph + v / SCH) + r of the tile.
@@ -1143,7 +1196,7 @@ __device__ __forceinline__ RowOffsets row_offsets(const AttnParams& p) {
 // When the tile starts a segment (with_q), Q_COPIES more copies per wave bring the Q operand rows
 // of the group's heads into the buffer's Q area: row r (clamped to R - 1) of head hg at
 // [hg][r], LDS chunk c holding global chunk c ^ (r % QCH).
-template <typename G, int POLICY = rows::kStreamPolicy>
+template <typename G, int POLICY = rows::kStreamPolicy, bool ROPE = false>
 __device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& d, bool with_q, char* buf,
                                            const RowOffsets& ro, int I0 = 0, int I1 = rows::TILE / 4) {
   const int lane = threadIdx.x & 63;
@@ -1196,6 +1249,13 @@ __device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& 
       const int gq = (lane % G::QCH) ^ (row % G::QCH);
       const uint16_t* src =
           p.q + d.b * p.q_sb + jq * p.q_ss + ((d.g * G::HG + hq_g) * p.g + hq) * p.q_sh + gq * 8;
+      if (ROPE && row >= p.R && row < p.R + 2 * p.s_q) {
+        // rotary: rows R + 2 j and R + 2 j + 1 of every head's area hold the cos and sin rows of
+        // position c + j (token j of this call)
+        const int jr = (row - p.R) >> 1;
+        const int pos = rope_position(p, d.c + jr);
+        src = ((row - p.R) & 1 ? p.rot_sin : p.rot_cos) + int64_t(pos) * G::HD + gq * 8;
+      }
       __builtin_amdgcn_global_load_lds(src, (rows::lds_void*)(buf + 2 * rows::TILE_BYTES + qi * 1024), 16, 0, 0);
     }
   }
@@ -1237,19 +1297,116 @@ __device__ __forceinline__ void rows_read_tile(const char* buf, int w, int s, in
   }
 }
 
+// Chunk ch of row `row` of group head hg's part of the buffer's Q area (stored at chunk
+// ch ^ (row % QCH)).
+template <typename G>
+__device__ __forceinline__ u32x4 q_area_chunk(const char* buf, int hg, int row, int ch) {
+  return *reinterpret_cast<const u32x4*>(buf + 2 * rows::TILE_BYTES + (hg * 16 + row) * G::QROW +
+                                         ((ch ^ (row % G::QCH)) << 4));
+}
+
 // Q^T operand (load_q's layout) of group head hg's rows from the buffer's Q area; rows li >= R
 // get 0.
 template <typename G>
 __device__ __forceinline__ void rows_read_q(const AttnParams& p, const char* buf, int hg,
                                             bf16x8 (&qf)[1][G::HD / 32]) {
+  constexpr int KK = G::HD / 32;
   const int lane = threadIdx.x & 63;
   const int li = lane & 15;
   const int lq = lane >> 4;
-  const char* qa = buf + 2 * rows::TILE_BYTES + (hg * 16 + li) * G::QROW;
 #pragma unroll
-  for (int kk = 0; kk < G::HD / 32; ++kk) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(qa + (((lq + 4 * kk) ^ (li % G::QCH)) << 4));
+  for (int kk = 0; kk < KK; ++kk) {
+    const u32x4 v = q_area_chunk<G>(buf, hg, li, lq + 4 * kk);
     qf[0][kk] = __builtin_bit_cast(bf16x8, li < p.R ? v : u32x4{0u, 0u, 0u, 0u});
+  }
+}
+
+// Rotary for the Q rows of a segment start in the buffer's Q area, in place: row r < R of head
+// hg (token j = r / g) with the cos / sin rows of its position, R + 2 j and R + 2 j + 1 of the
+// area.  The waves of head hg (one per phase) share its rows, lane (row, pair c) rotating chunk c
+// and its rotate_half partner c + HD/16: one chunk pair per lane at R <= 8, where rotating in
+// load_q's layout costs every lane HD/64 pairs for all 16 area rows (7B decode: 31.8 us per call
+// that way, against 29.3 us without rotary).  With phases the other waves of the head then read
+// what this one wrote, behind a barrier.
+template <typename G>
+__device__ __forceinline__ void rows_rope_q_area(const AttnParams& p, char* buf) {
+  constexpr int PC = G::HD / 16;  // chunk pairs per head row
+  constexpr int RPW = 64 / PC;    // rows per wave and pass
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int hg = w % G::HG;
+  const int ph = w / G::HG;
+  const int pc = lane % PC;
+  for (int r0 = ph * RPW; r0 < p.R; r0 += G::P * RPW) {
+    const int row = r0 + lane / PC;
+    if (row < p.R) {
+      const int rc = p.R + 2 * (row / p.g);
+      char* rb = buf + 2 * rows::TILE_BYTES + (hg * 16 + row) * G::QROW;
+      u32x4* pa = reinterpret_cast<u32x4*>(rb + ((pc ^ (row % G::QCH)) << 4));
+      u32x4* pb = reinterpret_cast<u32x4*>(rb + (((pc + PC) ^ (row % G::QCH)) << 4));
+      u32x4 a = *pa, b = *pb;
+      rope_pair(a, b, q_area_chunk<G>(buf, hg, rc, pc), q_area_chunk<G>(buf, hg, rc + 1, pc),
+                q_area_chunk<G>(buf, hg, rc, pc + PC), q_area_chunk<G>(buf, hg, rc + 1, pc + PC));
+      *pa = a;
+      *pb = b;
+    }
+  }
+  if constexpr (G::P > 1) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's rows are written
+    raw_barrier();
+  }
+}
+
+// Whether tile d's copies bring the buffer's Q area (Q in LDS): when the tile starts a segment,
+// and with rotary tables when it holds new rows, whose rotation needs the cos / sin rows there.
+template <typename G, bool ROPE>
+__device__ __forceinline__ bool q_area_copy(const AttnParams& p, const TileDesc& d, bool q_in_lds) {
+  return q_in_lds && (d.T0 == p.k0 || (ROPE && tile_has_new<G::TOK>(p, d)));
+}
+
+// Word wd (elements 2 wd, 2 wd + 1) of chunk ch of row `row` of group head hg's part of the
+// buffer's Q area.
+template <typename G>
+__device__ __forceinline__ uint32_t q_area_word(const char* buf, int hg, int row, int ch, int wd) {
+  return *reinterpret_cast<const uint32_t*>(buf + 2 * rows::TILE_BYTES + (hg * 16 + row) * G::QROW +
+                                            ((ch ^ (row % G::QCH)) << 4) + 4 * wd);
+}
+
+// Rotary for this call's new K rows of tile d in LDS buffer `buf` (wave w's slice: head hg, its
+// phase's tokens), before they are read or appended: lane (row t, word i of the first half)
+// rotates that word and its rotate_half partner HD/4 words on with the cos / sin rows of the
+// token's position from head hg's Q area -- a decode step's one new row spread over HD/4 lanes.
+template <typename G>
+__device__ __forceinline__ void rows_rope_new_k(const AttnParams& p, const TileDesc& d, char* buf) {
+  constexpr int PC = G::HD / 16;  // rotary chunk pairs per head row
+  constexpr int WPR = 4 * PC;     // word pairs per head row
+  constexpr int RPP = 64 / WPR;   // token rows per pass
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int hg = w % G::HG;
+  const int ph = w / G::HG;
+  const int pc = (lane % WPR) >> 2;
+  const int wd = lane & 3;
+#pragma unroll
+  for (int s = 0; s < G::S; ++s) {
+    const int T0s = d.T0 + rows::TILE * (ph * G::S + s);
+    const int t_lo = max(T0s, d.c);
+    const int t_hi = min(T0s + rows::TILE, d.L);
+    for (int t0 = t_lo; t0 < t_hi; t0 += RPP) {
+      const int t = t0 + lane / WPR;
+      if (t < t_hi) {
+        const int r = t - T0s;
+        const int rc = p.R + 2 * (t - d.c);
+        char* row = buf + r * rows::ROW_BYTES + w * 256;
+        uint32_t* pa = reinterpret_cast<uint32_t*>(row + (((s * G::SCH + pc) ^ rows::swz(r)) << 4) + 4 * wd);
+        uint32_t* pb = reinterpret_cast<uint32_t*>(row + (((s * G::SCH + pc + PC) ^ rows::swz(r)) << 4) + 4 * wd);
+        uint32_t a = *pa, b = *pb;
+        rope_word(a, b, q_area_word<G>(buf, hg, rc, pc, wd), q_area_word<G>(buf, hg, rc + 1, pc, wd),
+                  q_area_word<G>(buf, hg, rc, pc + PC, wd), q_area_word<G>(buf, hg, rc + 1, pc + PC, wd));
+        *pa = a;
+        *pb = b;
+      }
+    }
   }
 }
 
@@ -1655,13 +1812,14 @@ __device__ __forceinline__ void phase_merge(char* buf, float (&m_run)[NT], float
   }
 }
 
-template <int NT, int NCH, bool CASCADE_SUFFIX, typename G>
+template <int NT, int NCH, bool CASCADE_SUFFIX, typename G, bool ROPE = false>
 __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p) {
   constexpr int HD = G::HD;
   constexpr int DPL = HD / 16;
   constexpr int KK = HD / 32;
   constexpr int TOK = G::TOK;
   constexpr bool kQInLds = NT == 1;
+  constexpr bool kRope = ROPE && kQInLds;  // rotary of q and the new K rows (rot_cos / rot_sin)
   constexpr int kQCopies = kQInLds ? G::Q_COPIES : 0;
   constexpr int BUF = 2 * rows::TILE_BYTES + (kQInLds ? G::Q_BYTES : 0);  // K tile | V tile | Q
   constexpr int kPolicy = NT == 1 || CASCADE_SUFFIX ? rows::kStreamPolicy : rows::kVerifyPolicy;
@@ -1694,10 +1852,10 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   TileDesc dA = tile_desc(win, s);
   TileDesc dB = dA;
   const RowOffsets ro = row_offsets<G>(p);
-  rows_issue<G, kPolicy>(p, dA, kQInLds, lds, ro);
+  rows_issue<G, kPolicy, kRope>(p, dA, kQInLds, lds, ro);
   if (n > 1) {
     dB = tile_desc(win, s + 1);
-    rows_issue<G, kPolicy>(p, dB, kQInLds && dB.T0 == p.k0, lds + BUF, ro);
+    rows_issue<G, kPolicy, kRope>(p, dB, q_area_copy<G, kRope>(p, dB, kQInLds), lds + BUF, ro);
   }
 
   bf16x8 qf[NT][KK];
@@ -1717,6 +1875,11 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   int seg_T0 = 0;  // its first token
   int stores_prev = 0, stores_prev2 = 0;  // epilogue stores of iterations j-1 and j-2 (lower bounds)
   int pub_first = -1, pub_last = -1;  // segments (g * batch + b) of the partials in slots 2w, 2w + 1
+  // The rare branches of the tile loop (segment start, new rows, segment end, a window refresh)
+  // carry expect hints, so the block layout keeps one tile's common path in straight-line code:
+  // each workgroup runs only a few dozen tiles, and an instruction-cache miss behind the saturated
+  // HBM stream costs about a microsecond (config-5 verify 60.7 us per call with the hints; 62-68 us
+  // when an unrelated edit let the new-row copies fall inline ahead of the common path).
   for (int j = 0; j < n; ++j) {
     const TileDesc d = dA;
     char* buf = lds + (j & 1) * BUF;
@@ -1729,11 +1892,12 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     if (j + 1 >= n)
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     else
-      wait_vmcnt_at_most(16 + (dB.T0 == p.k0 ? kQCopies : 0) + stores_prev + stores_prev2);
+      wait_vmcnt_at_most(16 + (q_area_copy<G, kRope>(p, dB, kQInLds) ? kQCopies : 0) + stores_prev + stores_prev2);
     raw_barrier();  // ... and every other wave's
-    if (j == 0 || d.T0 == p.k0) {
+    if (__builtin_expect(j == 0 || d.T0 == p.k0, 0)) {
       // a segment starts: its Q operand, row limits and a fresh softmax state
       if constexpr (kQInLds) {
+        if constexpr (kRope) rows_rope_q_area<G>(p, buf);
         rows_read_q<G>(p, buf, hg, qf);
       } else {
         rows_load_q<HD, NT>(p, d, d.g * G::HG + hg, qf);
@@ -1760,7 +1924,10 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
       for (int off = 1; off < 16; off <<= 1) lim_min = min(lim_min, __shfl_xor(lim_min, off, 64));
       lim_min = __builtin_amdgcn_readfirstlane(lim_min);
     }
-    if (tile_has_new<TOK>(p, d)) rows_append_from_lds<G>(p, d, buf);
+    if (__builtin_expect(tile_has_new<TOK>(p, d), 0)) {
+      if constexpr (kRope) rows_rope_new_k<G>(p, d, buf);
+      rows_append_from_lds<G>(p, d, buf);
+    }
     KVTile<HD> tl[G::S];
 #pragma unroll
     for (int sub = 0; sub < G::S; ++sub)
@@ -1779,9 +1946,9 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     const bool next2 = j + 2 < n;
     if (next2) {
       const int x2 = s + j + 2;
-      if (x2 - win.x0 >= 64) tile_window<NCH, TOK>(p, st, x2, e, T1, win);
+      if (__builtin_expect(x2 - win.x0 >= 64, 0)) tile_window<NCH, TOK>(p, st, x2, e, T1, win);
       d2 = tile_desc(win, x2);
-      if (!defer) rows_issue<G, kPolicy>(p, d2, false, buf, ro, 0, 4);
+      if (!defer) rows_issue<G, kPolicy, kRope>(p, d2, false, buf, ro, 0, 4);
     }
     dA = dB;
     dB = d2;
@@ -1797,14 +1964,14 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
           compute_tile<HD, NT, true>(p, tl[sub], T0s, qf, lim, lim_min, m_run, l_run, acc);
       }
     }
-    if (next2 && !defer) rows_issue<G, kPolicy>(p, d2, kQInLds && d2.T0 == p.k0, buf, ro, 4, 8);
+    if (next2 && !defer) rows_issue<G, kPolicy, kRope>(p, d2, q_area_copy<G, kRope>(p, d2, kQInLds), buf, ro, 4, 8);
 
     stores_prev2 = stores_prev;
     stores_prev = 0;
-    if (!seg_end) continue;  // the segment goes on
+    if (__builtin_expect(!seg_end, 1)) continue;  // the segment goes on
     if constexpr (G::P > 1) {
       phase_merge<G, NT>(buf, m_run, l_run, acc);
-      if (next2) rows_issue<G, kPolicy>(p, d2, kQInLds && d2.T0 == p.k0, buf, ro);
+      if (next2) rows_issue<G, kPolicy, kRope>(p, d2, q_area_copy<G, kRope>(p, d2, kQInLds), buf, ro);
       if (!leader) continue;  // the phase-0 wave of each head holds the merged state
     }
     // ---- segment epilogue: wave (hg, phase 0) owns head hg's rows li + 16 nt < R (per N tile 4
@@ -2579,6 +2746,15 @@ static int lean_grid(int32_t flags) {
 template <int NT, bool CS, typename G>
 static void launch_lean_nt(const AttnParams& p, int batch, int grid, hipStream_t s) {
   const int wgs = grid + (p.two_pass ? 0 : batch * p.n_kv * ((p.R + 3) / 4));
+  if constexpr (NT == 1 && !CS) {
+    if (p.rot_cos) {  // a separate kernel: the rotary code costs the plain decode a few tenths of a us
+      if (batch <= 64)
+        decode_lean_kernel<NT, 1, CS, G, true><<<wgs, 256, 0, s>>>(p);
+      else
+        decode_lean_kernel<NT, rows::kChunks, CS, G, true><<<wgs, 256, 0, s>>>(p);
+      return;
+    }
+  }
   if (batch <= 64)
     decode_lean_kernel<NT, 1, CS, G><<<wgs, 256, 0, s>>>(p);
   else
@@ -2706,6 +2882,9 @@ static void fill_params(AttnParams& p, const void* q, int64_t q_sb, int64_t q_ss
   p.n_groups = 1;
   p.tok_elems = 0;  // set by the balanced-kernel launches
   p.cnt_stride = 1;
+  p.rot_cos = nullptr;
+  p.rot_sin = nullptr;
+  p.n_pos = 0;
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
 }
 
@@ -2837,7 +3016,8 @@ static int decode_attn(const char* fn, bool use_scratch, const void* q, int64_t 
                        void* workspace, size_t workspace_bytes, int32_t batch, int32_t s_q, int32_t n_heads,
                        int32_t n_kv, int32_t head_dim, int32_t page_size, int32_t num_pages, int32_t max_blocks,
                        int32_t causal, float softmax_scale, int32_t split_tokens, int32_t flags, int32_t* status,
-                       void* stream) {
+                       void* stream, const void* rot_cos = nullptr, const void* rot_sin = nullptr,
+                       int32_t n_pos = 0) {
   int rc = validate_attn(fn, q, q_sb, q_ss, q_sh, k_new, kn_sb, kn_ss, kn_sh, v_new, vn_sb, vn_ss, vn_sh, k_cache,
                          v_cache, cache_page_stride, block_table, bt_stride, cache_seqlens, out, o_sb, o_ss, o_sh,
                          batch, s_q, n_heads, n_kv, head_dim, page_size, num_pages, max_blocks, softmax_scale);
@@ -2851,6 +3031,18 @@ static int decode_attn(const char* fn, bool use_scratch, const void* q, int64_t 
   if (split_tokens < 0 || split_tokens % 32)
     return fail(PKV_EINVAL, "%s: split_tokens %d must be 0 or a positive multiple of 32", fn, split_tokens);
   const bool lean = use_lean_kernel(batch, head_dim, n_kv, R, page_size, split_tokens, flags);
+  if (rot_cos || rot_sin) {
+    // rotary is applied by the balanced kernel as it stages Q and the new rows: its cos / sin rows
+    // share the Q area of 16 rows per KV head with the R query rows (2 rows per new token)
+    if (!rot_cos || !rot_sin || n_pos <= 0 || !aligned16(rot_cos) || !aligned16(rot_sin))
+      return fail(PKV_EINVAL, "%s: cos / sin tables must be 16-byte aligned [n_pos >= 1, head_dim]", fn);
+    if (!k_new) return fail(PKV_EINVAL, "%s: rotary needs the new k / v rows", fn);
+    if (!lean || R + 2 * s_q > 16)
+      return fail(PKV_EINVAL, "%s: rotary is fused into the balanced decode kernel only (head_dim 128, or 64 with "
+                  "an even n_kv; page_size a tile or more; batch <= 256; s_q * n_heads / n_kv + 2 s_q <= 16 = %d; "
+                  "no split_tokens or PKV_DECODE_HEADS): rotate with pkv_rope_qk and call pkv_decode_attn",
+                  fn, R + 2 * s_q);
+  }
   const int st = split_tokens > 0 ? split_tokens : kHeadSplitDefault;
   const int64_t ms = max_splits_for(st, page_size, max_blocks);
   if (ms > 65535) return fail(PKV_EINVAL, "%s: %lld splits exceed the grid limit", fn, (long long)ms);
@@ -2884,6 +3076,9 @@ static int decode_attn(const char* fn, bool use_scratch, const void* q, int64_t 
               cache_page_stride, block_table, bt_stride, cache_seqlens, out, o_sb, o_ss, o_sh, s_q, n_heads, n_kv,
               page_size, num_pages, max_blocks, causal, softmax_scale, status);
   p.batch = batch;
+  p.rot_cos = static_cast<const uint16_t*>(rot_cos);
+  p.rot_sin = static_cast<const uint16_t*>(rot_sin);
+  p.n_pos = n_pos;
   if (lean) {
     // balanced row-streaming kernel; partials merged by a second launch, or inside the launch
     // with PKV_DECODE_FUSED_MERGE (slower on the 7B decode step: the merge of a long sequence's
@@ -2936,6 +3131,24 @@ extern "C" int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_
                           out, o_sb, o_ss, o_sh, workspace, workspace_bytes, batch, s_q, n_heads, n_kv, head_dim,
                           page_size, num_pages, max_blocks, causal, softmax_scale, split_tokens, flags, status,
                           stream);
+}
+
+extern "C" int pkv_decode_attn_rope(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, const void* k_new,
+                                    int64_t kn_sb, int64_t kn_ss, int64_t kn_sh, const void* v_new, int64_t vn_sb,
+                                    int64_t vn_ss, int64_t vn_sh, void* k_cache, void* v_cache,
+                                    int64_t cache_page_stride, const int32_t* block_table, int64_t bt_stride,
+                                    const int32_t* cache_seqlens, const void* cos_tab, const void* sin_tab,
+                                    int32_t n_pos, void* out, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+                                    void* workspace, size_t workspace_bytes, int32_t batch, int32_t s_q,
+                                    int32_t n_heads, int32_t n_kv, int32_t head_dim, int32_t page_size,
+                                    int32_t num_pages, int32_t max_blocks, int32_t causal, float softmax_scale,
+                                    int32_t flags, int32_t* status, void* stream) {
+  pkv::clear_error();
+  return pkv::decode_attn("pkv_decode_attn_rope", false, q, q_sb, q_ss, q_sh, k_new, kn_sb, kn_ss, kn_sh, v_new,
+                          vn_sb, vn_ss, vn_sh, k_cache, v_cache, cache_page_stride, block_table, bt_stride,
+                          cache_seqlens, out, o_sb, o_ss, o_sh, workspace, workspace_bytes, batch, s_q, n_heads,
+                          n_kv, head_dim, page_size, num_pages, max_blocks, causal, softmax_scale, 0, flags, status,
+                          stream, cos_tab, sin_tab, n_pos);
 }
 
 extern "C" int pkv_decode_attn_noalloc(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh, const void* k_new,

@@ -86,6 +86,75 @@ def test_rope_qk_appends_into_pages_then_attends(gpu):
     assert prism_amd.read_status(gpu) == 0
 
 
+ROPE_ATTN_CASES = [
+    # (batch, ctx, page, n_kv, n_heads, hd, s_q, grid, two_pass)
+    (32, [(i * 397) % 3000 for i in range(32)], 256, 4, 28, 128, 1, 0, None),   # 7B decode
+    (32, [(i * 397) % 3000 for i in range(32)], 256, 4, 28, 128, 1, 9, False),  # in-launch merge
+    (6, [3000, 17, 4100, 800, 1, 2500], 256, 8, 40, 128, 2, 0, None),          # 14B, 2 new rows, R = 10
+    (6, [3000, 17, 4100, 800, 1, 2500], 256, 2, 14, 64, 1, 7, None),           # 0.5B (hd 64, two phases)
+    (6, [3000, 17, 4100, 800, 1, 2500], 256, 1, 7, 128, 1, 5, None),           # 7B on 4 TP ranks
+    (40, [(i * 37) % 300 for i in range(40)], 64, 2, 14, 128, 1, 3, None),     # 64-token pages, 2 phases
+    (3, [0, 255, 256], 256, 4, 28, 128, 1, 0, None),                           # page edges, empty cache
+]
+
+
+@pytest.mark.parametrize("case", ROPE_ATTN_CASES, ids=[f"r{i}" for i in range(len(ROPE_ATTN_CASES))])
+def test_rope_decode_attention_matches_the_reference_step(gpu, case):
+    # one launch for the reference's q / k rotation, append and paged attention: the cache rows
+    # bit-identical to the reference expression's (and so to rope_qk's), the output within the
+    # attention tolerance of the fp64 oracle and of the two-launch path (rope_qk + attention)
+    B, ctx, P, nkv, nh, hd, s, grid, two_pass = case
+    print(f"rope_decode_attention B={B} P={P} kv={nkv} h={nh} hd={hd} s={s} grid={grid}", flush=True)
+    cpu, dev = make_paged_case(gpu, batch=B, ctx=ctx, page_size=P, n_kv=nkv, n_heads=nh, head_dim=hd, s_q=s,
+                               seed=B + nkv)
+    qkv = _rand((B, s, (nh + 2 * nkv) * hd), 31 + nkv, 1.0)
+    pos = np.array(ctx, dtype=np.int32)
+    cos, sin = ep.rope_tables(hd, 8192)
+    q_ref, k_ref, v_ref = ep.qkv_split_rope(qkv, pos, cos, sin, nh, nkv)
+    ref, kb, vb = pa.flash_attn_with_kvcache_ref(q_ref, cpu["k_cache"], cpu["v_cache"], k_ref, v_ref,
+                                                 cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"],
+                                                 causal=True)
+    dcos, dsin = cos.to(gpu), sin.to(gpu)
+    kc0, vc0 = dev["k_cache"].clone(), dev["v_cache"].clone()
+    out = torch.full((B, s, nh, hd), float("nan"), dtype=torch.bfloat16, device=gpu)
+    prism_amd.rope_decode_attention(qkv.to(gpu), dev["k_cache"], dev["v_cache"], dcos, dsin,
+                                    cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"],
+                                    n_heads=nh, n_kv=nkv, grid=grid, two_pass=two_pass, out=out)
+    torch.cuda.synchronize()
+    assert prism_amd.read_status(gpu) == 0
+    assert np.array_equal(pa.bf16_bits(dev["k_cache"]), kb), "appended (rotated) K not bit-exact"
+    assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "appended V not bit-exact"
+    assert_attn_close(out, ref, f"rope_decode_attention {case[:1] + case[2:]}")
+    sl = dev["cache_seqlens"]
+    q2, _ = prism_amd.rope_qk(qkv.to(gpu), sl, dcos, dsin, nh, nkv, return_k=False, k_cache=kc0, v_cache=vc0,
+                              block_table=dev["block_table"], cache_seqlens=sl)
+    two = prism_amd.flash_attn_with_kvcache(q2, kc0, vc0, cache_seqlens=sl + s, block_table=dev["block_table"],
+                                            causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(kc0, dev["k_cache"]) and torch.equal(vc0, dev["v_cache"]), "caches differ from rope_qk's"
+    assert float((two.float() - out.float()).abs().max()) <= 1e-2
+
+
+def test_rope_decode_attention_flags_positions_and_rejects_other_shapes(gpu):
+    B, nh, nkv, hd, P = 2, 28, 4, 128, 256
+    cpu, dev = make_paged_case(gpu, batch=B, ctx=[10, 40], page_size=P, n_kv=nkv, n_heads=nh, head_dim=hd, s_q=1,
+                               seed=3)
+    qkv = _rand((B, 1, (nh + 2 * nkv) * hd), 4).to(gpu)
+    cos, sin = prism_amd.rope_tables(hd, 32, device=gpu)   # position 40 is past the table
+    prism_amd.rope_decode_attention(qkv, dev["k_cache"], dev["v_cache"], cos, sin,
+                                    cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"],
+                                    n_heads=nh, n_kv=nkv)
+    torch.cuda.synchronize()
+    assert prism_amd.read_status(gpu) == prism_amd._lib.PKV_STATUS_BAD_POSITION
+    # verify rows (R + 2 s_q > 16) are not fused: the call is refused before anything runs
+    cpu, dev = make_paged_case(gpu, batch=B, ctx=[10, 40], page_size=P, n_kv=nkv, n_heads=nh, head_dim=hd, s_q=3,
+                               seed=3)
+    with pytest.raises(prism_amd._lib.PrismKVError, match="fused into the balanced decode kernel"):
+        prism_amd.rope_decode_attention(_rand((B, 3, (nh + 2 * nkv) * hd), 5).to(gpu), dev["k_cache"],
+                                        dev["v_cache"], cos, sin, cache_seqlens=dev["cache_seqlens"],
+                                        block_table=dev["block_table"], n_heads=nh, n_kv=nkv)
+
+
 def test_device_rope_tables_match_the_cpu_formula(gpu):
     # the reference builds its tables on the device (engine/executor.py:49-55); device and host
     # cos / sin may differ in the last fp32 bit, so bf16 entries agree to one unit
