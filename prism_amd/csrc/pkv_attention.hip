@@ -394,6 +394,13 @@ constexpr float kRescaleSlack = 8.0f;
 #ifndef PKV_PREFILL_DEPTH
 #define PKV_PREFILL_DEPTH 1
 #endif
+// prefill's software pipeline, and the vector instructions between its interleaved MFMAs
+#ifndef PKV_PREFILL_PIPE
+#define PKV_PREFILL_PIPE 1
+#endif
+#ifndef PKV_PREFILL_PIPE_VALU
+#define PKV_PREFILL_PIPE_VALU 2
+#endif
 constexpr int kDecodeDepth = PKV_DECODE_DEPTH;
 constexpr int kPrefillDepth = PKV_PREFILL_DEPTH;
 
@@ -2276,17 +2283,9 @@ __device__ __forceinline__ void pf_wait(int ahead) {
 // of a row at the end) or the whole row sum kept by the matrix cores (f32x4: P times a ones
 // operand, every element the row's sum, of the same bf16 P the PV product uses), which takes the
 // 16 additions per tile off the vector ALU for NT extra products.
-template <int NT, typename LT, typename VIssue, typename VOps>
-__device__ __forceinline__ void compute_tile_prefill_ops(const AttnParams& p, const u32x4 (&kr)[2][4],
-                                                         VIssue&& v_issue, VOps&& v_ops, int T0,
-                                                         const bf16x8 (&qf)[NT][4],
-                                                         const int (&lim)[NT], int lim_min, float (&m_run)[NT],
-                                                         LT (&l_run)[NT], f32x4 (&acc)[NT][8]) {
-  constexpr bool kLByMfma = std::is_same<LT, f32x4>::value;
-  constexpr int DPL = 8;
-  const int lane = threadIdx.x & 63;
-  const int lq = lane >> 4;
-  f32x4 s[NT][2];
+// S^T products of a tile: NT x 2 independent chains of 4 MFMAs over the head dimension.
+template <int NT>
+__device__ __forceinline__ void pf_qk(const u32x4 (&kr)[2][4], const bf16x8 (&qf)[NT][4], f32x4 (&s)[NT][2]) {
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -2297,7 +2296,22 @@ __device__ __forceinline__ void compute_tile_prefill_ops(const AttnParams& p, co
         s[nt][a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[a][kk]), qf[nt][kk],
                                                            s[nt][a], 0, 0, 0);
     }
-  v_issue();
+}
+
+// The rest of the update from the scores s: mask, rescale, P, row sums and PV.  With NEXT, the
+// next tile's S^T products (K operands kn, into sn) go out interleaved with this tile's
+// exponentials, one MFMA between every few vector instructions: a wave issues in order and its
+// next MFMA waits for the matrix pipe, so products placed back to back would hold the softmax
+// behind them, while interleaved the two pipes work at once.
+template <int NT, bool NEXT, typename LT, typename VOps>
+__device__ __forceinline__ void pf_softmax_pv(const AttnParams& p, f32x4 (&s)[NT][2], const u32x4 (&kn)[2][4],
+                                              f32x4 (&sn)[NT][2], VOps&& v_ops, int T0, const bf16x8 (&qf)[NT][4],
+                                              const int (&lim)[NT], int lim_min, float (&m_run)[NT],
+                                              LT (&l_run)[NT], f32x4 (&acc)[NT][8]) {
+  constexpr bool kLByMfma = std::is_same<LT, f32x4>::value;
+  constexpr int DPL = 8;
+  const int lane = threadIdx.x & 63;
+  const int lq = lane >> 4;
   if (T0 + 31 > lim_min) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
@@ -2346,6 +2360,25 @@ __device__ __forceinline__ void compute_tile_prefill_ops(const AttnParams& p, co
     if constexpr (!kLByMfma) l_run[nt] += psum;
     pb[nt] = __builtin_bit_cast(bf16x8, pk);
   }
+  if constexpr (NEXT) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int a = 0; a < 2; ++a) sn[nt][a] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+          sn[nt][a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kn[a][kk]), qf[nt][kk],
+                                                              sn[nt][a], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 8 * NT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, PKV_PREFILL_PIPE_VALU, 0);  // then vector ALU work
+    }
+  }
   if constexpr (kLByMfma) {
     const u32x4 one2 = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0 pairs
 #pragma unroll
@@ -2359,6 +2392,19 @@ __device__ __forceinline__ void compute_tile_prefill_ops(const AttnParams& p, co
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
       acc[nt][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[n], pb[nt], acc[nt][n], 0, 0, 0);
+}
+
+template <int NT, typename LT, typename VIssue, typename VOps>
+__device__ __forceinline__ void compute_tile_prefill_ops(const AttnParams& p, const u32x4 (&kr)[2][4],
+                                                         VIssue&& v_issue, VOps&& v_ops, int T0,
+                                                         const bf16x8 (&qf)[NT][4],
+                                                         const int (&lim)[NT], int lim_min, float (&m_run)[NT],
+                                                         LT (&l_run)[NT], f32x4 (&acc)[NT][8]) {
+  f32x4 s[NT][2];
+  pf_qk<NT>(kr, qf, s);
+  v_issue();
+  f32x4 sn_unused[NT][2];
+  pf_softmax_pv<NT, false>(p, s, kr, sn_unused, v_ops, T0, qf, lim, lim_min, m_run, l_run, acc);
 }
 
 // The same update on a tile read row-wise (KVTile): V^T operand n of lane (i, q) is head-dim
@@ -2545,22 +2591,14 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
 #pragma unroll
     for (int n = 0; n < DPL; ++n) acc[nt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  for (int st = 0; st < n_stages; ++st) {
-    if constexpr (kOneBarrier) {
-      pf_wait<OPS, NBUF>(min(NBUF - 2, n_stages - 1 - st));
-      raw_barrier();
-      if (st + NBUF - 1 < n_stages) issue(st + NBUF - 1);
-    } else {
-      pf_wait<OPS, NBUF>(min(NBUF - 1, n_stages - 1 - st));
-      raw_barrier();
-    }
-#pragma unroll
-    for (int u = 0; u < SUB; ++u) {
-      const int t = st * SUB + u;
-      if (t >= n_tiles) break;
-      const int T0 = (t_first + t) * pf::TILE;
-      const char* buf = lds + ((st % NBUF) * SUB + u) * pf::BUF;
-      u32x4 kr[2][4];
+  // Software pipeline (one tile per stage, NBUF >= 3): tile t's softmax and PV products run with
+  // tile t + 1's S^T products interleaved, so every iteration first waits for stage t + 1.  After
+  // that wait's barrier no wave reads stage t - 1 any more (its K went into the products of
+  // iteration t - 2, its V into those of t - 1), so stage t + NBUF - 1 is issued into its buffer.
+  constexpr bool kPipe = kOneBarrier && SUB == 1 && PKV_PREFILL_PIPE;
+  if constexpr (kPipe) {
+    auto read_k = [&](int t, u32x4 (&kr)[2][4]) {
+      const char* buf = lds + (t % NBUF) * pf::BUF;
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         const int r = 8 * (li >> 2) + 4 * a + (li & 3);
@@ -2568,19 +2606,31 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
         for (int kk = 0; kk < 4; ++kk)
           kr[a][kk] = *reinterpret_cast<const u32x4*>(buf + r * pf::ROW + (((4 * kk + lq) ^ rows::swz(r)) << 4));
       }
-      // the V^T reads go out once the QK products are issued (so the compiler's waits for the K
-      // reads, which do not count these, stay exact) and are waited for just before the PV
-      // products (lds_tr_wait): their latency hides behind the QK products and the softmax
-      const uint32_t vrows = lds_addr(buf + pf::KV_BYTES);
+    };
+    f32x4 s[NT][2];
+    pf_wait<OPS, NBUF>(min(NBUF - 2, n_stages - 1));
+    raw_barrier();
+    if (row0 < R_all && n_tiles > 0) {
+      u32x4 kr[2][4];
+      read_k(0, kr);
+      pf_qk<NT>(kr, qf, s);
+    }
+    // tile t's update, with tile t + 1's products when NEXT
+    auto step = [&](int t, auto next) {
+      constexpr bool NEXT = decltype(next)::value;
+      if (row0 >= R_all) return;
+      const int T0 = (t_first + t) * pf::TILE;
+      const uint32_t vrows = lds_addr(lds + (t % NBUF) * pf::BUF + pf::KV_BYTES);
       u32x2 vlo[8], vhi[8];
-      auto v_issue = [&] {
-        __builtin_amdgcn_sched_barrier(0);
+      // the V^T reads go out before the next tile's K reads, so the compiler's own wait for
+      // those (it does not count these) also covers them
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int n = 0; n < 8; ++n) {
-          vlo[n] = lds_read_tr16_issue<0>(vrows + vtr[n]);
-          vhi[n] = lds_read_tr16_issue<4 * pf::ROW>(vrows + vtr[n]);
-        }
-      };
+      for (int n = 0; n < 8; ++n) {
+        vlo[n] = lds_read_tr16_issue<0>(vrows + vtr[n]);
+        vhi[n] = lds_read_tr16_issue<4 * pf::ROW>(vrows + vtr[n]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
       auto v_ops = [&](bf16x8 (&vt)[8]) {
         lds_tr_wait(vlo, vhi);
         u32x4 vw[8];
@@ -2599,12 +2649,86 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
 #pragma unroll
         for (int n = 0; n < 8; ++n) vt[n] = __builtin_bit_cast(bf16x8, vw[n]);
       };
-      if (row0 < R_all) compute_tile_prefill_ops<NT>(p, kr, v_issue, v_ops, T0, qf, lim, lim_min, m_run, l_run, acc);
+      u32x4 kn[2][4];
+      f32x4 sn[NT][2];
+      if constexpr (NEXT) read_k(t + 1, kn);
+      pf_softmax_pv<NT, NEXT>(p, s, kn, sn, v_ops, T0, qf, lim, lim_min, m_run, l_run, acc);
+      if constexpr (NEXT) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+          for (int a = 0; a < 2; ++a) s[nt][a] = sn[nt][a];
+      }
+    };
+    for (int t = 0; t + 1 < n_tiles; ++t) {
+      pf_wait<OPS, NBUF>(min(NBUF - 3, n_stages - 2 - t));
+      raw_barrier();
+      if (t + NBUF - 1 < n_stages) issue(t + NBUF - 1);
+      step(t, std::true_type{});
     }
-    if constexpr (!kOneBarrier) {
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the stage are done
-      raw_barrier();                       // the stage's buffer is free
-      if (st + NBUF < n_stages) issue(st + NBUF);
+    if (n_tiles > 0) step(n_tiles - 1, std::false_type{});
+  } else {
+    for (int st = 0; st < n_stages; ++st) {
+      if constexpr (kOneBarrier) {
+        pf_wait<OPS, NBUF>(min(NBUF - 2, n_stages - 1 - st));
+        raw_barrier();
+        if (st + NBUF - 1 < n_stages) issue(st + NBUF - 1);
+      } else {
+        pf_wait<OPS, NBUF>(min(NBUF - 1, n_stages - 1 - st));
+        raw_barrier();
+      }
+  #pragma unroll
+      for (int u = 0; u < SUB; ++u) {
+        const int t = st * SUB + u;
+        if (t >= n_tiles) break;
+        const int T0 = (t_first + t) * pf::TILE;
+        const char* buf = lds + ((st % NBUF) * SUB + u) * pf::BUF;
+        u32x4 kr[2][4];
+  #pragma unroll
+        for (int a = 0; a < 2; ++a) {
+          const int r = 8 * (li >> 2) + 4 * a + (li & 3);
+  #pragma unroll
+          for (int kk = 0; kk < 4; ++kk)
+            kr[a][kk] = *reinterpret_cast<const u32x4*>(buf + r * pf::ROW + (((4 * kk + lq) ^ rows::swz(r)) << 4));
+        }
+        // the V^T reads go out once the QK products are issued (so the compiler's waits for the K
+        // reads, which do not count these, stay exact) and are waited for just before the PV
+        // products (lds_tr_wait): their latency hides behind the QK products and the softmax
+        const uint32_t vrows = lds_addr(buf + pf::KV_BYTES);
+        u32x2 vlo[8], vhi[8];
+        auto v_issue = [&] {
+          __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+          for (int n = 0; n < 8; ++n) {
+            vlo[n] = lds_read_tr16_issue<0>(vrows + vtr[n]);
+            vhi[n] = lds_read_tr16_issue<4 * pf::ROW>(vrows + vtr[n]);
+          }
+        };
+        auto v_ops = [&](bf16x8 (&vt)[8]) {
+          lds_tr_wait(vlo, vhi);
+          u32x4 vw[8];
+  #pragma unroll
+          for (int n = 0; n < 8; ++n) vw[n] = u32x4{vlo[n][0], vlo[n][1], vhi[n][0], vhi[n][1]};
+          if (T0 + pf::TILE > L) {
+            // keys past the sequence: P = 0 must not meet a stale NaN (word w holds keys 2 w, 2 w + 1)
+  #pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              const int k = T0 + 8 * lq + 2 * w;
+              const uint32_t keep = (k < L ? 0x0000FFFFu : 0u) | (k + 1 < L ? 0xFFFF0000u : 0u);
+  #pragma unroll
+              for (int n = 0; n < 8; ++n) vw[n][w] &= keep;
+            }
+          }
+  #pragma unroll
+          for (int n = 0; n < 8; ++n) vt[n] = __builtin_bit_cast(bf16x8, vw[n]);
+        };
+        if (row0 < R_all) compute_tile_prefill_ops<NT>(p, kr, v_issue, v_ops, T0, qf, lim, lim_min, m_run, l_run, acc);
+      }
+      if constexpr (!kOneBarrier) {
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the stage are done
+        raw_barrier();                       // the stage's buffer is free
+        if (st + NBUF < n_stages) issue(st + NBUF);
+      }
     }
   }
   if (row0 >= R_all) return;
