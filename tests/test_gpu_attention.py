@@ -152,6 +152,7 @@ GEOM_CASES = [
     (40, [(i * 37) % 300 for i in range(40)], 128, 1, 7, 128, 1, 5, True),
     (40, [(i * 37) % 300 for i in range(40)], 64, 2, 14, 128, 1, 3, True),
     (40, [(i * 37) % 300 for i in range(40)], 128, 2, 14, 64, 1, 11, True),
+    (70, [(i * 53) % 900 for i in range(70)], 256, 8, 40, 128, 1, 0, True),  # 14B, over 64 sequences
     (5, [10, 2000, 130, 40, 250], 128, 3, 21, 128, 1, 3, True),           # 3 groups of 1
     (5, [10, 2000, 130, 40, 250], 64, 6, 24, 128, 2, 4, True),            # 3 groups of 2
     (5, [10, 2000, 130, 40, 250], 64, 4, 16, 64, 1, 2, True),             # hd 64, one group of 4

@@ -95,6 +95,8 @@ ROPE_ATTN_CASES = [
     (6, [3000, 17, 4100, 800, 1, 2500], 256, 1, 7, 128, 1, 5, None),           # 7B on 4 TP ranks
     (40, [(i * 37) % 300 for i in range(40)], 64, 2, 14, 128, 1, 3, None),     # 64-token pages, 2 phases
     (3, [0, 255, 256], 256, 4, 28, 128, 1, 0, None),                           # page edges, empty cache
+    (70, [(i * 53) % 900 for i in range(70)], 256, 4, 28, 128, 1, 0, None),    # over 64 sequences
+    (70, [(i * 53) % 900 for i in range(70)], 256, 2, 14, 64, 1, 0, None),
 ]
 
 
