@@ -1289,17 +1289,26 @@ __device__ __forceinline__ void rows_read_tile(const char* buf, int w, int s, in
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int r = 8 * lq + e;
-    const bool keep = T0s + r < t_end;  // rows past the sequence: P = 0 must not meet a stale NaN
     if constexpr (G::HD == 128) {
       const int chunk = w * 16 + (li ^ rows::swz(r));
       const u32x4 v = *reinterpret_cast<const u32x4*>(vb + r * rows::ROW_BYTES + chunk * 16);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) tl.vr[e].w[k] = keep ? v[k] : 0u;
+      for (int k = 0; k < 4; ++k) tl.vr[e].w[k] = v[k];
     } else {
       const int chunk = w * 16 + ((s * G::SCH + (li >> 1)) ^ rows::swz(r));
       const u32x2 v = *reinterpret_cast<const u32x2*>(vb + r * rows::ROW_BYTES + chunk * 16 + (li & 1) * 8);
-      tl.vr[e].w[0] = keep ? v[0] : 0u;
-      tl.vr[e].w[1] = keep ? v[1] : 0u;
+      tl.vr[e].w[0] = v[0];
+      tl.vr[e].w[1] = v[1];
+    }
+  }
+  // rows past the sequence: P = 0 must not meet a stale NaN (only a sequence's last subtile has
+  // them, so the selects stay off the common path)
+  if (__builtin_expect(T0s + rows::TILE > t_end, 0)) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool keep = T0s + 8 * lq + e < t_end;
+#pragma unroll
+      for (int k = 0; k < G::HD / 32; ++k) tl.vr[e].w[k] = keep ? tl.vr[e].w[k] : 0u;
     }
   }
 }

@@ -14,10 +14,29 @@ from pkv_testutil import assert_attn_close, make_paged_case
 pytestmark = pytest.mark.gpu
 
 
+def _poison_stale_slots(cpu, dev, ctx):
+    """NaN into every cache slot that holds no cached key: the slots past each sequence's keys
+    (the appended rows included) and the pages no sequence lists.  Whole tiles are copied into
+    LDS, so those bytes reach the kernels; none may reach an output."""
+    kc, bt = cpu["k_cache"], cpu["block_table"].numpy()
+    num_pages, P = kc.shape[:2]
+    live = np.zeros((num_pages, P), dtype=bool)
+    for b, c in enumerate(ctx):
+        for t in range(int(c)):
+            live[bt[b, t // P], t % P] = True
+    stale = torch.from_numpy(~live)
+    for name in ("k_cache", "v_cache"):
+        cpu[name][stale] = float("nan")
+        dev[name].copy_(cpu[name].to(dev[name].device))
+
+
 def _run_and_check(gpu, *, batch, ctx, page_size, n_kv, n_heads, head_dim, s_q, causal=True, append=True,
-                   split_tokens=0, seed=0, kernel="auto", extra_cols=0, two_pass=None, grid=0, what=""):
+                   split_tokens=0, seed=0, kernel="auto", extra_cols=0, two_pass=None, grid=0, what="",
+                   poison=False):
     cpu, dev = make_paged_case(gpu, batch=batch, ctx=ctx, page_size=page_size, n_kv=n_kv, n_heads=n_heads,
                                head_dim=head_dim, s_q=s_q, seed=seed, extra_cols=extra_cols)
+    if poison:
+        _poison_stale_slots(cpu, dev, ctx)
     print(f"case {what} B={batch} ctx={list(ctx)[:6]} P={page_size} kv={n_kv} h={n_heads} hd={head_dim} "
           f"s_q={s_q} causal={causal} append={append} split={split_tokens} kernel={kernel} two_pass={two_pass} "
           f"grid={grid}",
@@ -62,6 +81,25 @@ def test_decode_append_attention(gpu, case):
     B, ctx, P, n_kv, nh, hd, s_q = case
     _run_and_check(gpu, batch=B, ctx=ctx, page_size=P, n_kv=n_kv, n_heads=nh, head_dim=hd, s_q=s_q,
                    what=f"decode{case}")
+
+
+STALE_NAN_CASES = [
+    # (batch, ctx, page, n_kv, n_heads, hd, s_q, kernel): every sequence ends inside a tile
+    (4, [1, 300, 1023, 517], 256, 4, 28, 128, 1, "auto"),     # 7B decode, balanced kernel
+    (3, [517, 2, 90], 256, 4, 28, 128, 5, "auto"),            # verify rows
+    (2, [700, 5], 32, 8, 40, 128, 1, "auto"),                 # 14B, two head groups
+    (4, [1, 300, 1023, 517], 256, 2, 14, 64, 1, "auto"),      # head_dim 64
+    (3, [517, 2, 90], 256, 4, 28, 128, 1, "heads"),           # per-head kernel
+    (2, [100, 1000], 64, 4, 4, 128, 1, "auto"),               # g = 1
+    (2, [200, 37], 256, 4, 28, 128, 64, "prefill"),           # prefill chunk
+]
+
+
+@pytest.mark.parametrize("case", STALE_NAN_CASES, ids=[f"n{i}" for i in range(len(STALE_NAN_CASES))])
+def test_stale_nan_slots_never_reach_the_output(gpu, case):
+    B, ctx, P, n_kv, nh, hd, s_q, kernel = case
+    _run_and_check(gpu, batch=B, ctx=ctx, page_size=P, n_kv=n_kv, n_heads=nh, head_dim=hd, s_q=s_q,
+                   kernel=kernel, poison=True, what=f"stale-nan{case}")
 
 
 @pytest.mark.parametrize("split", [32, 64, 256, 1 << 20])
