@@ -2927,6 +2927,10 @@ static void launch_lean(const AttnParams& p, int head_dim, int R, int batch, int
     default: break;
   }
 }
+// Merge mode of a balanced call without a merge flag: in the launch when the block table's
+// capacity is at most this many tiles per workgroup.
+constexpr int kFusedMaxTilesPerWg = 6;
+
 static int lean_heads_per_group(int head_dim, int n_kv) {
   switch (lean_geom(head_dim, n_kv)) {
     case kGeom128x4: case kGeom64x4: return 4;
@@ -3220,8 +3224,21 @@ static int decode_attn(const char* fn, bool use_scratch, const void* q, int64_t 
     p.ws_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
     p.ws_ml = lean_lse_base(p.ws_o, size_t(2) * grid, R);
     // in-launch merge only for decode rows (R <= 16): verify's row count would need too many
-    // merge workgroups, so it always merges in a second launch
-    p.two_pass = merge == PKV_DECODE_FUSED_MERGE && R <= 16 ? 0 : 1;
+    // merge workgroups, so it always merges in a second launch.  Without a merge flag the call
+    // merges in the launch when the block table bounds it to kFusedMaxTilesPerWg tiles per
+    // workgroup: such a call is bound by fixed costs, and the in-launch merge saves the second
+    // launch's (7B at B = 8, 0.5B and 7B TP-4 shards of a 32-sequence ragged batch: 17.3-17.5 /
+    // 15.6 / 18.4 us per call against 17.5-17.6 / 16.1-16.3 / 19.6 two-pass), while the longer
+    // streams of bigger calls finish sooner with the second launch (7B at B = 32: 29.5 against
+    // 28.8-29.3, 14B: 47.2-48.1 against 46.3).
+    bool fused = merge == PKV_DECODE_FUSED_MERGE;
+    if (merge == 0) {
+      const int hg = lean_heads_per_group(head_dim, n_kv);
+      const int64_t tok = int64_t(rows::TILE) * (4 / hg) * (128 / head_dim);  // tokens per tile
+      const int64_t tiles = int64_t(n_kv / hg) * batch * ((int64_t(max_blocks) * page_size + tok - 1) / tok);
+      fused = tiles <= int64_t(kFusedMaxTilesPerWg) * grid;
+    }
+    p.two_pass = fused && R <= 16 ? 0 : 1;
     // the counters 128 bytes apart where the counter region has room
     p.cnt_stride = 1;
     while (p.cnt_stride < 32 && int64_t(batch) * n_kv * p.cnt_stride * 2 <= kMaxCounters) p.cnt_stride *= 2;
