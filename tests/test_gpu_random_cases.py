@@ -1,0 +1,58 @@
+"""Seeded random sweep of the drop-in attention op against the fp64 oracle (through the C ABI).
+
+Each case draws a batch, ragged context lengths (zeros included), a page size, a Qwen2.5 head
+geometry (whole model or a tensor-parallel shard), s_q, causal or not, append or not, and a
+fragmented page pool; the library picks its kernel and merge as it would for Prism.  Checked:
+outputs within the north_star bf16 tolerance of the fp64 oracle, and both caches bit-exact after
+the append (whole pools compared).  The draws are fixed by the seed list, so a failure names a
+reproducible case.
+"""
+import numpy as np
+import pytest
+import torch
+
+import prism_amd
+from oracle import paged_attention as pa
+from pkv_testutil import assert_attn_close, make_paged_case
+
+pytestmark = pytest.mark.gpu
+
+# (n_heads, n_kv, head_dim): Qwen2.5 0.5B / 7B / 14B and their tensor-parallel shards
+GEOMETRIES = [(14, 2, 64), (7, 1, 64), (28, 4, 128), (14, 2, 128), (7, 1, 128), (40, 8, 128), (20, 4, 128),
+              (10, 2, 128)]
+PAGE_SIZES = [16, 32, 64, 128, 256]
+S_Q = [1, 1, 1, 2, 4, 5]
+
+
+def draw(seed):
+    rng = np.random.default_rng(1000 + seed)
+    nh, n_kv, hd = GEOMETRIES[rng.integers(len(GEOMETRIES))]
+    batch = int(rng.integers(1, 41))
+    ctx = rng.integers(0, 3000, size=batch)
+    ctx[rng.random(batch) < 0.1] = 0
+    return dict(batch=batch, ctx=[int(c) for c in ctx], page_size=int(PAGE_SIZES[rng.integers(len(PAGE_SIZES))]),
+                n_kv=n_kv, n_heads=nh, head_dim=hd, s_q=int(S_Q[rng.integers(len(S_Q))]),
+                causal=bool(rng.random() < 0.8), append=bool(rng.random() < 0.8), seed=seed)
+
+
+@pytest.mark.parametrize("seed", range(48))
+def test_random_case_matches_oracle(gpu, seed):
+    c = draw(seed)
+    print(f"random case {seed}: B={c['batch']} ctx[:6]={c['ctx'][:6]} P={c['page_size']} h={c['n_heads']} "
+          f"kv={c['n_kv']} hd={c['head_dim']} s_q={c['s_q']} causal={c['causal']} append={c['append']}", flush=True)
+    cpu, dev = make_paged_case(gpu, batch=c["batch"], ctx=c["ctx"], page_size=c["page_size"], n_kv=c["n_kv"],
+                               n_heads=c["n_heads"], head_dim=c["head_dim"], s_q=c["s_q"], seed=seed)
+    k = dev["k"] if c["append"] else None
+    v = dev["v"] if c["append"] else None
+    out = torch.full_like(dev["q"], float("nan"))
+    out = prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], k, v,
+                                            cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"],
+                                            causal=c["causal"], out=out)
+    torch.cuda.synchronize()
+    ref, kb, vb = pa.flash_attn_with_kvcache_ref(
+        cpu["q"], cpu["k_cache"], cpu["v_cache"], cpu["k"] if c["append"] else None,
+        cpu["v"] if c["append"] else None, cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"],
+        causal=c["causal"])
+    assert np.array_equal(pa.bf16_bits(dev["k_cache"]), kb), "K cache not bit-exact after append"
+    assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "V cache not bit-exact after append"
+    assert_attn_close(out, ref, f"random case {seed}")
