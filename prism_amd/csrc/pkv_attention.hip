@@ -233,6 +233,14 @@ __device__ __forceinline__ int bt_page(const AttnParams& p, const SeqView& sv, i
   return __builtin_amdgcn_readlane(w.ids, col - w.col0);
 }
 
+// The last visible key of a padding row (a row past the real query rows, computed and never
+// stored).  Real rows keep their own limit, negative when they see no key (causal rows of a call
+// whose keys are fewer than its queries), and only padding rows are left out of the wave's
+// minimum limit, which decides whether a tile needs the mask at all.
+constexpr int kNoQueryRow = INT_MIN;
+
+__device__ __forceinline__ int min_real_limit(int acc, int lim) { return min(acc, lim == kNoQueryRow ? INT_MAX : lim); }
+
 // Load the Q^T operand for the 16*NT rows starting at row0 and the last key each row may see.
 template <int HD, int NT>
 __device__ __forceinline__ void load_q(const AttnParams& p, const SeqView& sv, int L, int row0,
@@ -254,7 +262,7 @@ __device__ __forceinline__ void load_q(const AttnParams& p, const SeqView& sv, i
     } else {
 #pragma unroll
       for (int kk = 0; kk < HD / 32; ++kk) qf[nt][kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
-      lim[nt] = -1;
+      lim[nt] = kNoQueryRow;
     }
   }
 }
@@ -282,7 +290,7 @@ __device__ __forceinline__ void load_q_batch_rows(const AttnParams& p, int h, in
     } else {
 #pragma unroll
       for (int kk = 0; kk < HD / 32; ++kk) qf[nt][kk] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
-      lim[nt] = -1;
+      lim[nt] = kNoQueryRow;
     }
   }
 }
@@ -519,7 +527,7 @@ __device__ __forceinline__ void wave_attend(const AttnParams& p, const SeqView& 
   int lim_min = 0x7fffffff;
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) lim_min = min(lim_min, lim[nt] < 0 ? 0x7fffffff : lim[nt]);
+  for (int nt = 0; nt < NT; ++nt) lim_min = min_real_limit(lim_min, lim[nt]);
 #pragma unroll
   for (int off = 1; off < 16; off <<= 1) lim_min = min(lim_min, __shfl_xor(lim_min, off, 64));
   lim_min = __builtin_amdgcn_readfirstlane(lim_min);
@@ -1881,7 +1889,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   f32x4 acc[NT][DPL];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    lim[nt] = -1;
+    lim[nt] = kNoQueryRow;
     m_run[nt] = -INFINITY;
     l_run[nt] = 0.f;
 #pragma unroll
@@ -1924,13 +1932,13 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int rr = li + 16 * nt;
-        lim[nt] = -1;
+        lim[nt] = kNoQueryRow;
         if (rr < p.R) {
           const int jr = rr / p.g;
           const int last = p.causal ? (d.L - p.s_q + jr) : (d.L - 1);
           lim[nt] = min(last, d.L - 1);
         }
-        lim_min = min(lim_min, lim[nt] < 0 ? 0x7fffffff : lim[nt]);
+        lim_min = min_real_limit(lim_min, lim[nt]);
         m_run[nt] = -INFINITY;
         l_run[nt] = 0.f;
 #pragma unroll
@@ -2525,7 +2533,7 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   int lim_min = 0x7fffffff;
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) lim_min = min(lim_min, lim[nt] < 0 ? 0x7fffffff : lim[nt]);
+  for (int nt = 0; nt < NT; ++nt) lim_min = min_real_limit(lim_min, lim[nt]);
 #pragma unroll
   for (int off = 1; off < 16; off <<= 1) lim_min = min(lim_min, __shfl_xor(lim_min, off, 64));
   lim_min = __builtin_amdgcn_readfirstlane(lim_min);

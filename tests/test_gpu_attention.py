@@ -102,6 +102,27 @@ def test_stale_nan_slots_never_reach_the_output(gpu, case):
                    kernel=kernel, poison=True, what=f"stale-nan{case}")
 
 
+FEWER_KEYS_CASES = [
+    # (batch, ctx, page, n_kv, n_heads, hd, s_q, kernel): no append, causal, fewer cached keys than
+    # queries, so the first rows see no key while later rows of the same wave see some
+    (2, [21, 80], 32, 2, 10, 128, 256, "auto"),   # prefill, LDS kernel
+    (2, [21, 80], 64, 2, 14, 64, 128, "auto"),    # prefill, head_dim 64 kernel
+    (3, [2, 4, 0], 256, 4, 28, 128, 5, "auto"),   # verify rows, balanced kernel
+    (3, [2, 4, 0], 256, 4, 28, 128, 5, "heads"),  # verify rows, per-head kernel
+    (2, [3, 1], 256, 1, 7, 128, 2, "auto"),       # a one-head shard
+]
+
+
+@pytest.mark.parametrize("case", FEWER_KEYS_CASES, ids=[f"f{i}" for i in range(len(FEWER_KEYS_CASES))])
+def test_rows_that_see_no_key_beside_rows_that_do(gpu, case):
+    """Rows with no visible key get zeros although other rows of their wave see keys: such a row
+    is part of the wave's decision to mask a tile (a negative limit), not left out of it like the
+    padding rows past the real ones."""
+    B, ctx, P, n_kv, nh, hd, s_q, kernel = case
+    _run_and_check(gpu, batch=B, ctx=ctx, page_size=P, n_kv=n_kv, n_heads=nh, head_dim=hd, s_q=s_q, append=False,
+                   kernel=kernel, what=f"fewer-keys{case}")
+
+
 @pytest.mark.parametrize("split", [32, 64, 256, 1 << 20])
 def test_decode_split_invariance(gpu, split):
     _run_and_check(gpu, batch=3, ctx=[1500, 33, 700], page_size=256, n_kv=4, n_heads=28, head_dim=128, s_q=1,

@@ -1,8 +1,8 @@
 """Seeded random sweep of the drop-in attention op against the fp64 oracle (through the C ABI).
 
 Each case draws a batch, ragged context lengths (zeros included), a page size, a Qwen2.5 head
-geometry (whole model or a tensor-parallel shard), s_q, causal or not, append or not, and a
-fragmented page pool; the library picks its kernel and merge as it would for Prism.  Checked:
+geometry (whole model or a tensor-parallel shard), s_q (decode and verify rows, or prefill
+chunks of 16-512 tokens), causal or not, append or not, and a fragmented page pool; the library picks its kernel and merge as it would for Prism.  Checked:
 outputs within the north_star bf16 tolerance of the fp64 oracle, and both caches bit-exact after
 the append (whole pools compared).  The draws are fixed by the seed list, so a failure names a
 reproducible case.
@@ -56,3 +56,39 @@ def test_random_case_matches_oracle(gpu, seed):
     assert np.array_equal(pa.bf16_bits(dev["k_cache"]), kb), "K cache not bit-exact after append"
     assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "V cache not bit-exact after append"
     assert_attn_close(out, ref, f"random case {seed}")
+
+
+def draw_prefill(seed):
+    rng = np.random.default_rng(5000 + seed)
+    nh, n_kv, hd = GEOMETRIES[rng.integers(len(GEOMETRIES))]
+    batch = int(rng.integers(1, 7))
+    ctx = rng.integers(0, 2500, size=batch)
+    ctx[rng.random(batch) < 0.2] = 0
+    s_q = int([16, 33, 64, 100, 128, 256, 512][rng.integers(7)])
+    return dict(batch=batch, ctx=[int(c) for c in ctx], page_size=int(PAGE_SIZES[rng.integers(len(PAGE_SIZES))]),
+                n_kv=n_kv, n_heads=nh, head_dim=hd, s_q=s_q, causal=bool(rng.random() < 0.85),
+                append=bool(rng.random() < 0.85), seed=seed)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_prefill_chunk_matches_oracle(gpu, seed):
+    """Chunks (s_q * n_heads / n_kv > 64) take the prefill kernels through the same drop-in call."""
+    c = draw_prefill(seed)
+    print(f"random prefill case {seed}: B={c['batch']} ctx={c['ctx']} P={c['page_size']} h={c['n_heads']} "
+          f"kv={c['n_kv']} hd={c['head_dim']} s_q={c['s_q']} causal={c['causal']} append={c['append']}", flush=True)
+    cpu, dev = make_paged_case(gpu, batch=c["batch"], ctx=c["ctx"], page_size=c["page_size"], n_kv=c["n_kv"],
+                               n_heads=c["n_heads"], head_dim=c["head_dim"], s_q=c["s_q"], seed=seed)
+    k = dev["k"] if c["append"] else None
+    v = dev["v"] if c["append"] else None
+    out = torch.full_like(dev["q"], float("nan"))
+    out = prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], k, v,
+                                            cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"],
+                                            causal=c["causal"], out=out)
+    torch.cuda.synchronize()
+    ref, kb, vb = pa.flash_attn_with_kvcache_ref(
+        cpu["q"], cpu["k_cache"], cpu["v_cache"], cpu["k"] if c["append"] else None,
+        cpu["v"] if c["append"] else None, cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"],
+        causal=c["causal"])
+    assert np.array_equal(pa.bf16_bits(dev["k_cache"]), kb), "K cache not bit-exact after append"
+    assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "V cache not bit-exact after append"
+    assert_attn_close(out, ref, f"random prefill case {seed}")
