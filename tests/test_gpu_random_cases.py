@@ -127,3 +127,47 @@ def test_random_cascade_matches_oracle(gpu, seed):
     assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "V cache not bit-exact after append"
     assert_attn_close(out, ref, f"random cascade case {seed}")
     assert prism_amd.read_status(gpu) == 0
+
+
+def draw_rope(seed):
+    rng = np.random.default_rng(13000 + seed)
+    # shapes the fused rotary launch takes: R + 2 s_q <= 16 rows per KV head, a page of a tile or more
+    nh, n_kv, hd = [(28, 4, 128), (40, 8, 128), (14, 2, 128), (7, 1, 128), (14, 2, 64), (20, 4, 128)][rng.integers(6)]
+    g = nh // n_kv
+    s_q = 2 if g <= 5 and rng.random() < 0.4 else 1
+    heads_per_tile = 4 if n_kv % 4 == 0 else (2 if n_kv % 2 == 0 else 1)
+    tile = 32 * (4 // heads_per_tile) * (128 // hd)  # tokens per tile of the balanced kernel
+    P = int(max(tile, [32, 64, 128, 256][rng.integers(4)]))
+    batch = int(rng.integers(1, 49))
+    ctx = rng.integers(0, 3000, size=batch)
+    ctx[rng.random(batch) < 0.1] = 0
+    return dict(batch=batch, ctx=[int(c) for c in ctx], page_size=P, n_kv=n_kv, n_heads=nh, head_dim=hd, s_q=s_q,
+                seed=seed)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_rope_decode_matches_reference_step(gpu, seed):
+    """The fused rotary + append + attention launch against the reference's bf16 rotary expression
+    and the fp64 attention oracle."""
+    from oracle import epilogue as ep
+    c = draw_rope(seed)
+    B, nh, nkv, hd, s = c["batch"], c["n_heads"], c["n_kv"], c["head_dim"], c["s_q"]
+    print(f"random rope case {seed}: B={B} P={c['page_size']} h={nh} kv={nkv} hd={hd} s_q={s}", flush=True)
+    cpu, dev = make_paged_case(gpu, batch=B, ctx=c["ctx"], page_size=c["page_size"], n_kv=nkv, n_heads=nh,
+                               head_dim=hd, s_q=s, seed=seed)
+    g = torch.Generator().manual_seed(77 + seed)
+    qkv = torch.randn((B, s, (nh + 2 * nkv) * hd), generator=g).to(torch.bfloat16)
+    cos, sin = ep.rope_tables(hd, 4096)
+    q_ref, k_ref, v_ref = ep.qkv_split_rope(qkv, np.array(c["ctx"], dtype=np.int32), cos, sin, nh, nkv)
+    ref, kb, vb = pa.flash_attn_with_kvcache_ref(q_ref, cpu["k_cache"], cpu["v_cache"], k_ref, v_ref,
+                                                 cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"],
+                                                 causal=True)
+    out = torch.full((B, s, nh, hd), float("nan"), dtype=torch.bfloat16, device=gpu)
+    prism_amd.rope_decode_attention(qkv.to(gpu), dev["k_cache"], dev["v_cache"], cos.to(gpu), sin.to(gpu),
+                                    cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"],
+                                    n_heads=nh, n_kv=nkv, out=out)
+    torch.cuda.synchronize()
+    assert prism_amd.read_status(gpu) == 0
+    assert np.array_equal(pa.bf16_bits(dev["k_cache"]), kb), "appended (rotated) K not bit-exact"
+    assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "appended V not bit-exact"
+    assert_attn_close(out, ref, f"random rope case {seed}")
