@@ -171,3 +171,40 @@ def test_random_rope_decode_matches_reference_step(gpu, seed):
     assert np.array_equal(pa.bf16_bits(dev["k_cache"]), kb), "appended (rotated) K not bit-exact"
     assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "appended V not bit-exact"
     assert_attn_close(out, ref, f"random rope case {seed}")
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_page_copies_match_oracle(gpu, seed):
+    """Batched page copies between two caches (whole or partial pages, direct and staged), whole
+    pools bit-exact against oracle/page_ops.py."""
+    from oracle import page_ops
+    from prism_amd import FlashAttnKVCache
+    rng = np.random.default_rng(17000 + seed)
+    layers = int(rng.integers(1, 5))
+    P = int([16, 32, 64, 256][rng.integers(4)])
+    n_kv, hd = [(2, 64), (4, 128), (8, 128), (1, 128)][rng.integers(4)]
+    pages = int(rng.integers(8, 60))
+    n = int(rng.integers(1, pages // 2 + 1))
+    staged = bool(rng.random() < 0.3)
+    print(f"random page copies {seed}: layers={layers} P={P} kv={n_kv} hd={hd} pages={pages} n={n} staged={staged}",
+          flush=True)
+    caches = []
+    for k in range(2):
+        kv = FlashAttnKVCache(layers, n_kv, hd, pages, P, str(gpu), torch.bfloat16)
+        g = torch.Generator(device=gpu).manual_seed(seed * 2 + k)
+        kv.k_pool.normal_(generator=g)
+        kv.v_pool.normal_(generator=g)
+        caches.append(kv)
+    src, dst = caches
+    src_ids = [int(x) for x in rng.choice(pages, size=n, replace=False)]
+    dst_ids = [int(x) for x in rng.choice(pages, size=n, replace=False)]
+    fill = [int(x) for x in rng.integers(1, P + 1, size=n)] if rng.random() < 0.6 else None
+    pools = lambda kv: [pa.bf16_bits(t) for t in kv.k_caches] + [pa.bf16_bits(t) for t in kv.v_caches]
+    before_src, before_dst = pools(src), pools(dst)
+    prism_amd.copy_pages(src, dst, src_ids, dst_ids, fill, staged=staged)
+    torch.cuda.synchronize()
+    expect = page_ops.copy_pages(before_src, before_dst, src_ids, dst_ids, fill)
+    for got, exp in zip(pools(dst), expect):
+        assert np.array_equal(got, exp)
+    for got, exp in zip(pools(src), before_src):
+        assert np.array_equal(got, exp), "source pool changed"
