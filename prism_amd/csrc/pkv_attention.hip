@@ -805,7 +805,9 @@ __global__ __launch_bounds__(512) void combine_kernel(const AttnParams p) {
   const int lr = threadIdx.x / Q4;
   const int row = rg + lr;
   const int d0 = (threadIdx.x - lr * Q4) * 4;
-  const bool active = row < p.R;
+  // 512 threads cover 512 / Q4 rows: 16 at head_dim 128, 32 at head_dim 64, where the upper half
+  // (rows of the next workgroup) only helps stage the (m, l) pairs
+  const bool active = lr < 16 && row < p.R;
   const int64_t base = int64_t(b * p.n_kv + h) * p.max_splits * p.R;
   if (threadIdx.x < 16) {
     sm_m[threadIdx.x] = -INFINITY;

@@ -123,6 +123,15 @@ def test_rows_that_see_no_key_beside_rows_that_do(gpu, case):
                    kernel=kernel, what=f"fewer-keys{case}")
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("s_q", [3, 8])
+def test_per_head_two_pass_merge_above_16_rows(gpu, hd, s_q):
+    """The per-head kernel's second-launch merge at more than 16 query rows per KV head: its
+    512 threads cover 32 rows at head_dim 64, of which a workgroup owns 16."""
+    _run_and_check(gpu, batch=6, ctx=[0, 0, 2356, 1300, 0, 2014], page_size=128, n_kv=2, n_heads=14, head_dim=hd,
+                   s_q=s_q, split_tokens=64, kernel="heads", two_pass=True, what=f"heads-two-pass hd={hd} s_q={s_q}")
+
+
 @pytest.mark.parametrize("split", [32, 64, 256, 1 << 20])
 def test_decode_split_invariance(gpu, split):
     _run_and_check(gpu, batch=3, ctx=[1500, 33, 700], page_size=256, n_kv=4, n_heads=28, head_dim=128, s_q=1,

@@ -208,3 +208,56 @@ def test_random_page_copies_match_oracle(gpu, seed):
         assert np.array_equal(got, exp)
     for got, exp in zip(pools(src), before_src):
         assert np.array_equal(got, exp), "source pool changed"
+
+
+def draw_options(seed):
+    rng = np.random.default_rng(21000 + seed)
+    nh, n_kv, hd = GEOMETRIES[rng.integers(len(GEOMETRIES))]
+    g = nh // n_kv
+    s_q = int(rng.integers(1, 64 // g + 1))
+    batch = int(rng.integers(1, 33))
+    ctx = rng.integers(0, 2500, size=batch)
+    ctx[rng.random(batch) < 0.1] = 0
+    return dict(batch=batch, ctx=[int(c) for c in ctx], page_size=int(PAGE_SIZES[rng.integers(len(PAGE_SIZES))]),
+                n_kv=n_kv, n_heads=nh, head_dim=hd, s_q=s_q, causal=bool(rng.random() < 0.7),
+                append=bool(rng.random() < 0.8), kernel=["auto", "auto", "heads"][rng.integers(3)],
+                split=int([0, 0, 32, 64, 256, 4096][rng.integers(6)]),
+                two_pass=[None, None, True, False][rng.integers(4)],
+                # an explicit scale around the default 1/sqrt(head_dim) (Prism passes the default;
+                # the bf16 P of the PV product puts scales several times larger past 1e-2)
+                scale=None if rng.random() < 0.5 else float(rng.uniform(0.5, 1.5) / np.sqrt(hd)),
+                strided=bool(rng.random() < 0.5), seed=seed)
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_call_options_match_oracle(gpu, seed):
+    """The decode / verify call with the options Prism and flash_attn expose: split lengths, the
+    per-head kernel, either merge, an explicit softmax scale, q / k / v as strided views of one
+    fused projection buffer, and up to 64 query rows per KV head."""
+    c = draw_options(seed)
+    B, nh, n_kv, hd, s = c["batch"], c["n_heads"], c["n_kv"], c["head_dim"], c["s_q"]
+    print(f"random options case {seed}: {c}", flush=True)
+    cpu, dev = make_paged_case(gpu, batch=B, ctx=c["ctx"], page_size=c["page_size"], n_kv=n_kv, n_heads=nh,
+                               head_dim=hd, s_q=s, seed=seed)
+    q, k, v = dev["q"], dev["k"], dev["v"]
+    if c["strided"]:
+        qs, kvs = nh * hd, n_kv * hd
+        qkv = torch.cat([q.reshape(B, s, qs), k.reshape(B, s, kvs), v.reshape(B, s, kvs)], dim=-1)
+        q = qkv[:, :, :qs].view(B, s, nh, hd)
+        k = qkv[:, :, qs:qs + kvs].view(B, s, n_kv, hd)
+        v = qkv[:, :, qs + kvs:].view(B, s, n_kv, hd)
+    if not c["append"]:
+        k = v = None
+    out = torch.full_like(dev["q"], float("nan"))
+    out = prism_amd.flash_attn_with_kvcache(q, dev["k_cache"], dev["v_cache"], k, v,
+                                            cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"],
+                                            causal=c["causal"], softmax_scale=c["scale"], split_tokens=c["split"],
+                                            kernel=c["kernel"], two_pass=c["two_pass"], out=out)
+    torch.cuda.synchronize()
+    ref, kb, vb = pa.flash_attn_with_kvcache_ref(
+        cpu["q"], cpu["k_cache"], cpu["v_cache"], cpu["k"] if c["append"] else None,
+        cpu["v"] if c["append"] else None, cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"],
+        causal=c["causal"], softmax_scale=c["scale"])
+    assert np.array_equal(pa.bf16_bits(dev["k_cache"]), kb), "K cache not bit-exact after append"
+    assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "V cache not bit-exact after append"
+    assert_attn_close(out, ref, f"random options case {seed}")
