@@ -261,3 +261,83 @@ def test_random_call_options_match_oracle(gpu, seed):
     assert np.array_equal(pa.bf16_bits(dev["k_cache"]), kb), "K cache not bit-exact after append"
     assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "V cache not bit-exact after append"
     assert_attn_close(out, ref, f"random options case {seed}")
+
+
+def _ulp_close(got, ref, what, ulps=1.0):
+    g = got.float().cpu().numpy().astype(np.float64)
+    tol = ulps * np.maximum(np.abs(ref), 1e-30) * 2.0 ** -7 + 1e-30
+    bad = np.abs(g - ref) > tol
+    assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} beyond {ulps} bf16 unit(s)"
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_epilogue_kernels_match_oracle(gpu, seed):
+    """rope_qk (bit-exact to the reference's bf16 expression), add + RMSNorm and SiLU-mul (within one
+    bf16 unit of fp64) at random row counts and widths, strided gate / up views included."""
+    from oracle import epilogue as ep
+    rng = np.random.default_rng(25000 + seed)
+    g = torch.Generator().manual_seed(seed)
+    rnd = lambda shape, scale=1.0: (torch.randn(shape, generator=g) * scale).to(torch.bfloat16)
+    nh, n_kv, hd = GEOMETRIES[rng.integers(len(GEOMETRIES))]
+    B, s = int(rng.integers(1, 65)), int([1, 1, 2, 5, 17, 64][rng.integers(6)])
+    print(f"random epilogue case {seed}: B={B} s={s} h={nh} kv={n_kv} hd={hd}", flush=True)
+    qkv = rnd((B, s, (nh + 2 * n_kv) * hd), 2.0)
+    pos = rng.integers(0, 6000, size=B).astype(np.int32)
+    cos, sin = ep.rope_tables(hd, 6100)
+    q_ref, k_ref, _ = ep.qkv_split_rope(qkv, pos, cos, sin, nh, n_kv)
+    q, k = prism_amd.rope_qk(qkv.to(gpu), torch.from_numpy(pos).to(gpu), cos.to(gpu), sin.to(gpu), nh, n_kv)
+    torch.cuda.synchronize()
+    assert torch.equal(q.cpu(), q_ref) and torch.equal(k.cpu(), k_ref), "rope_qk not bit-exact"
+    rows, hidden = int(rng.integers(1, 70)), int([896, 1536, 2048, 3584, 5120, 8192][rng.integers(6)])
+    x, w = rnd((rows, hidden), 3.0), rnd((hidden,))
+    resid = bool(rng.random() < 0.5)
+    r = rnd((rows, hidden)) if resid else None
+    ref, h_ref = ep.rms_norm_f64(x.float().numpy(), w.float().numpy(), 1e-6, r.float().numpy() if resid else None)
+    res = prism_amd.rms_norm(x.to(gpu), w.to(gpu), 1e-6, residual=r.to(gpu) if resid else None)
+    torch.cuda.synchronize()
+    _ulp_close(res[0] if resid else res, ep.round_bf16(ref), "rms_norm")
+    if resid:
+        assert np.array_equal(res[1].float().cpu().numpy(), h_ref), "residual sum not bit-exact"
+    m = int([4864, 8960, 13824, 18944, 1000][rng.integers(5)])
+    gu = rnd((rows, 2 * m), 3.0)
+    sref = ep.silu_mul_ref(gu[:, :m].float().numpy(), gu[:, m:].float().numpy())
+    d = gu.to(gpu)
+    out = prism_amd.silu_mul(d[:, :m], d[:, m:])
+    torch.cuda.synchronize()
+    _ulp_close(out, sref, "silu_mul")
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_launch_shapes_match_oracle(gpu, seed):
+    """The balanced kernel on an explicit number of workgroups (1 to 600, so ranges from hundreds
+    of tiles down to none), flash_attn's num_splits, and batches past the balanced kernel's 256."""
+    rng = np.random.default_rng(29000 + seed)
+    nh, n_kv, hd = GEOMETRIES[rng.integers(len(GEOMETRIES))]
+    g = nh // n_kv
+    s_q = int(rng.integers(1, 16 // g + 2)) if g < 16 else 1
+    mode = ["grid", "grid", "splits", "big"][rng.integers(4)]
+    batch = int(rng.integers(257, 301)) if mode == "big" else int(rng.integers(1, 41))
+    ctx = rng.integers(0, 600 if mode == "big" else 2500, size=batch)
+    ctx[rng.random(batch) < 0.1] = 0
+    heads_per_tile = 4 if n_kv % 4 == 0 else (2 if n_kv % 2 == 0 else 1)
+    P = int(max(32 * (4 // heads_per_tile) * (128 // hd), [16, 32, 64, 128, 256][rng.integers(5)]))
+    grid = int([1, 2, 3, 7, 33, 100, 256, 300, 600][rng.integers(9)]) if mode == "grid" else 0
+    num_splits = int(rng.integers(1, 9)) if mode == "splits" else 0
+    two_pass = [None, True, False][rng.integers(3)]
+    print(f"random launch case {seed}: mode={mode} B={batch} P={P} h={nh} kv={n_kv} hd={hd} s_q={s_q} grid={grid} "
+          f"num_splits={num_splits} two_pass={two_pass}", flush=True)
+    cpu, dev = make_paged_case(gpu, batch=batch, ctx=[int(c) for c in ctx], page_size=P, n_kv=n_kv, n_heads=nh,
+                               head_dim=hd, s_q=s_q, seed=seed)
+    out = torch.full_like(dev["q"], float("nan"))
+    out = prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], dev["k"], dev["v"],
+                                            cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"],
+                                            causal=True, grid=grid, num_splits=num_splits, two_pass=two_pass,
+                                            out=out)
+    torch.cuda.synchronize()
+    ref, kb, vb = pa.flash_attn_with_kvcache_ref(cpu["q"], cpu["k_cache"], cpu["v_cache"], cpu["k"], cpu["v"],
+                                                 cache_seqlens=cpu["cache_seqlens"],
+                                                 block_table=cpu["block_table"], causal=True)
+    assert np.array_equal(pa.bf16_bits(dev["k_cache"]), kb), "K cache not bit-exact after append"
+    assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "V cache not bit-exact after append"
+    assert_attn_close(out, ref, f"random launch case {seed}")
+    assert prism_amd.read_status(gpu) == 0
