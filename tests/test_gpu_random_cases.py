@@ -341,3 +341,34 @@ def test_random_launch_shapes_match_oracle(gpu, seed):
     assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "V cache not bit-exact after append"
     assert_attn_close(out, ref, f"random launch case {seed}")
     assert prism_amd.read_status(gpu) == 0
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_forced_prefill_kernel_matches_oracle(gpu, seed):
+    """prefill_attention (the row-parallel prefill kernels, whatever s_q) at small and odd shapes:
+    1-300 query tokens, causal or not, append or not, every page size and head geometry."""
+    rng = np.random.default_rng(33000 + seed)
+    nh, n_kv, hd = GEOMETRIES[rng.integers(len(GEOMETRIES))]
+    batch = int(rng.integers(1, 9))
+    ctx = rng.integers(0, 2000, size=batch)
+    ctx[rng.random(batch) < 0.2] = 0
+    s_q = int(rng.integers(1, 301))
+    P = int(PAGE_SIZES[rng.integers(len(PAGE_SIZES))])
+    causal, append = bool(rng.random() < 0.7), bool(rng.random() < 0.7)
+    print(f"random forced prefill case {seed}: B={batch} ctx={list(ctx)} P={P} h={nh} kv={n_kv} hd={hd} s_q={s_q} "
+          f"causal={causal} append={append}", flush=True)
+    cpu, dev = make_paged_case(gpu, batch=batch, ctx=[int(c) for c in ctx], page_size=P, n_kv=n_kv, n_heads=nh,
+                               head_dim=hd, s_q=s_q, seed=seed)
+    k = dev["k"] if append else None
+    v = dev["v"] if append else None
+    out = torch.full_like(dev["q"], float("nan"))
+    out = prism_amd.prefill_attention(dev["q"], dev["k_cache"], dev["v_cache"], k, v,
+                                      cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"],
+                                      causal=causal, out=out)
+    torch.cuda.synchronize()
+    ref, kb, vb = pa.flash_attn_with_kvcache_ref(
+        cpu["q"], cpu["k_cache"], cpu["v_cache"], cpu["k"] if append else None, cpu["v"] if append else None,
+        cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"], causal=causal)
+    assert np.array_equal(pa.bf16_bits(dev["k_cache"]), kb), "K cache not bit-exact after append"
+    assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "V cache not bit-exact after append"
+    assert_attn_close(out, ref, f"random forced prefill case {seed}")
