@@ -103,26 +103,27 @@ def draw_cascade(seed):
     suffix = rng.integers(0, 900, size=batch)
     suffix[rng.random(batch) < 0.15] = 0
     return dict(suffix=[int(x) for x in suffix], shared_pages=shared_pages, page_size=P,
-                s_q=int([1, 2, 4, 5, 8][rng.integers(5)]), n_heads=nh, n_kv=n_kv, hd=hd, seed=seed)
+                s_q=int([1, 2, 4, 5, 8][rng.integers(5)]), n_heads=nh, n_kv=n_kv, hd=hd, seed=seed,
+                causal=bool(rng.random() < 0.75))
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(32))
 def test_random_cascade_matches_oracle(gpu, seed):
     """Batches sharing a random number of prefix pages, declared through shared_prefix_tokens."""
     from test_gpu_cascade import _shared_case
     c = draw_cascade(seed)
     print(f"random cascade case {seed}: B={len(c['suffix'])} shared={c['shared_pages']}x{c['page_size']} "
-          f"h={c['n_heads']} kv={c['n_kv']} hd={c['hd']} s_q={c['s_q']}", flush=True)
+          f"h={c['n_heads']} kv={c['n_kv']} hd={c['hd']} s_q={c['s_q']} causal={c['causal']}", flush=True)
     cpu, dev, shared = _shared_case(gpu, suffix=c["suffix"], shared_pages=c["shared_pages"], page_size=c["page_size"],
                                     s_q=c["s_q"], n_heads=c["n_heads"], n_kv=c["n_kv"], hd=c["hd"], seed=seed)
     out = torch.full_like(dev["q"], float("nan"))
     prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], dev["k"], dev["v"],
                                       cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"],
-                                      causal=True, shared_prefix_tokens=shared, out=out)
+                                      causal=c["causal"], shared_prefix_tokens=shared, out=out)
     torch.cuda.synchronize()
     ref, kb, vb = pa.flash_attn_with_kvcache_ref(cpu["q"], cpu["k_cache"], cpu["v_cache"], cpu["k"], cpu["v"],
                                                  cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"],
-                                                 causal=True)
+                                                 causal=c["causal"])
     assert np.array_equal(pa.bf16_bits(dev["k_cache"]), kb), "K cache not bit-exact after append"
     assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "V cache not bit-exact after append"
     assert_attn_close(out, ref, f"random cascade case {seed}")
