@@ -373,3 +373,98 @@ def test_random_forced_prefill_kernel_matches_oracle(gpu, seed):
     assert np.array_equal(pa.bf16_bits(dev["k_cache"]), kb), "K cache not bit-exact after append"
     assert np.array_equal(pa.bf16_bits(dev["v_cache"]), vb), "V cache not bit-exact after append"
     assert_attn_close(out, ref, f"random forced prefill case {seed}")
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_cache_lifecycle_keeps_every_sequence_exact(gpu, seed):
+    """A random life of one FlashAttnKVCache on the device: sequences created, grown by decode and
+    chunk appends through the drop-in attention call (which appends), forked (shared pages,
+    copy-on-write on the next write), freed and compacted.  A host mirror keeps each sequence's
+    K / V rows; after every step each live sequence's rows, gathered through its page list, are
+    bit-identical to the mirror, and every attention output is bit-identical to the same call on
+    a fresh cache holding the mirror's rows in consecutive pages (the attention arithmetic itself
+    is checked against the oracle by the other sweeps)."""
+    from prism_amd import FlashAttnKVCache
+    rng = np.random.default_rng(37000 + seed)
+    nh, n_kv, hd = [(28, 4, 128), (14, 2, 64), (40, 8, 128), (7, 1, 128)][seed % 4]
+    P = int([16, 32, 64, 256][rng.integers(4)])
+    kv = FlashAttnKVCache(1, n_kv, hd, 160 if P >= 64 else 600, P, str(gpu), torch.bfloat16)
+    kv.k_pool.zero_()
+    kv.v_pool.zero_()
+    mirror_k: dict[int, np.ndarray] = {}
+    mirror_v: dict[int, np.ndarray] = {}
+    next_id = 0
+
+    def gather(sid):
+        L = kv.seq_len[sid]
+        pages = kv.seq_pages[sid]
+        kc, vc = pa.bf16_bits(kv.k_caches[0]), pa.bf16_bits(kv.v_caches[0])
+        rows = [(pages[t // P], t % P) for t in range(L)]
+        return (np.array([kc[p, r] for p, r in rows]).reshape(L, n_kv, hd),
+                np.array([vc[p, r] for p, r in rows]).reshape(L, n_kv, hd))
+
+    for step in range(14):
+        live = sorted(mirror_k)
+        op = rng.random()
+        if not live or (op < 0.25 and len(live) < 6):
+            kv.new_sequence(next_id)
+            kv.seq_len[next_id] = 0
+            mirror_k[next_id] = np.zeros((0, n_kv, hd), np.uint16)
+            mirror_v[next_id] = np.zeros((0, n_kv, hd), np.uint16)
+            next_id += 1
+        elif op < 0.35 and len(live) < 6:
+            src = int(rng.choice(live))
+            if kv.seq_len[src] > 0:
+                kv.fork_sequence(src, next_id)
+                mirror_k[next_id], mirror_v[next_id] = mirror_k[src].copy(), mirror_v[src].copy()
+                next_id += 1
+        elif op < 0.45 and len(live) > 1:
+            victim = int(rng.choice(live))
+            kv.free_sequence(victim)
+            del mirror_k[victim], mirror_v[victim]
+        elif op < 0.55:
+            kv.compact()
+        live = sorted(mirror_k)
+        # one attention call that appends s_q new rows to a batch of the live sequences
+        batch = [int(x) for x in rng.choice(live, size=int(rng.integers(1, len(live) + 1)), replace=False)]
+        s_q = int([1, 1, 1, 3, 17, 40][rng.integers(6)])
+        if kv.pages_free < len(batch) * (s_q // P + 2) + 2:
+            continue
+        kv.prepare_append(batch, s_q)
+        bt, sl = kv.build_block_table(batch)
+        g = torch.Generator().manual_seed(seed * 100 + step)
+        q = torch.randn(len(batch), s_q, nh, hd, generator=g).to(torch.bfloat16)
+        k = torch.randn(len(batch), s_q, n_kv, hd, generator=g).to(torch.bfloat16)
+        v = torch.randn(len(batch), s_q, n_kv, hd, generator=g).to(torch.bfloat16)
+        out = prism_amd.flash_attn_with_kvcache(q.to(gpu), kv.k_caches[0], kv.v_caches[0], k.to(gpu), v.to(gpu),
+                                                cache_seqlens=sl, block_table=bt, causal=True)
+        # the same call on a fresh cache holding the mirror's rows in consecutive pages: the kernels'
+        # arithmetic depends on lengths and token positions only, so the outputs must match bit for
+        # bit whatever pages, forks, copies and compactions the first cache went through
+        lens = [len(mirror_k[sid]) for sid in batch]
+        need = [-(-(L + s_q) // P) for L in lens]
+        fk = torch.zeros(sum(need), P, n_kv, hd, dtype=torch.bfloat16)
+        fv = torch.zeros_like(fk)
+        fbt = torch.zeros(len(batch), max(need), dtype=torch.int32)
+        base = 0
+        for i, sid in enumerate(batch):
+            L = lens[i]
+            fbt[i, :need[i]] = torch.arange(base, base + need[i], dtype=torch.int32)
+            rows_k = torch.from_numpy(mirror_k[sid].astype(np.int16)).view(torch.bfloat16)
+            rows_v = torch.from_numpy(mirror_v[sid].astype(np.int16)).view(torch.bfloat16)
+            fk.view(-1, n_kv, hd)[base * P: base * P + L] = rows_k
+            fv.view(-1, n_kv, hd)[base * P: base * P + L] = rows_v
+            base += need[i]
+        out2 = prism_amd.flash_attn_with_kvcache(q.to(gpu), fk.to(gpu), fv.to(gpu), k.to(gpu), v.to(gpu),
+                                                 cache_seqlens=torch.tensor(lens, dtype=torch.int32, device=gpu),
+                                                 block_table=fbt.to(gpu), causal=True)
+        torch.cuda.synchronize()
+        assert torch.equal(out, out2), f"lifecycle {seed} step {step}: output depends on the page layout"
+        kv.update_seqlens(batch, s_q)
+        for i, sid in enumerate(batch):
+            mirror_k[sid] = np.concatenate([mirror_k[sid], pa.bf16_bits(k[i])])
+            mirror_v[sid] = np.concatenate([mirror_v[sid], pa.bf16_bits(v[i])])
+        for sid in mirror_k:
+            gk, gv = gather(sid)
+            assert np.array_equal(gk, mirror_k[sid]) and np.array_equal(gv, mirror_v[sid]), \
+                f"lifecycle {seed} step {step}: sequence {sid} rows differ"
