@@ -1204,6 +1204,36 @@ __device__ __forceinline__ RowOffsets row_offsets(const AttnParams& p) {
   return ro;
 }
 
+// The rotary kernel's offsets: row_offsets' plus, per Q copy i, the element offset inside q of
+// the lane's chunk less the sequence and head-group terms (the query row and head a lane copies
+// are the same for every segment start of the launch).  Precomputed so the rotary instantiation
+// (more registers live than the plain one) does not redo the divisions by g at every segment.
+struct RowOffsetsQ : RowOffsets {
+  int64_t q[4];
+};
+
+template <typename G>
+__device__ __forceinline__ RowOffsetsQ row_offsets_q(const AttnParams& p) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  RowOffsetsQ ro;
+  static_cast<RowOffsets&>(ro) = row_offsets<G>(p);
+  static_assert(G::Q_COPIES <= 4, "Q copies per wave");
+#pragma unroll
+  for (int i = 0; i < G::Q_COPIES; ++i) {
+    const int qi = wave * G::Q_COPIES + i;
+    const int ar = qi * (1024 / G::QROW) + lane / G::QCH;
+    const int hq_g = ar / 16;
+    const int row = ar % 16;
+    const int rr = min(row, p.R - 1);
+    const int jq = rr / p.g;
+    const int hq = rr - jq * p.g;
+    const int gq = (lane % G::QCH) ^ (row % G::QCH);
+    ro.q[i] = jq * p.q_ss + int64_t(hq_g * p.g + hq) * p.q_sh + gq * 8;
+  }
+  return ro;
+}
+
 // Copies of tile d into LDS buffer `buf`, 16 per wave: K then V rows, wave w filling LDS rows
 // w, w + 4, ..., lane l writing LDS chunk l of a row (row_offsets' mapping).  A tile without new
 // rows is two buffers (its K and its V run, TOK token rows each, base and range in scalar
@@ -1213,9 +1243,9 @@ __device__ __forceinline__ RowOffsets row_offsets(const AttnParams& p) {
 // When the tile starts a segment (with_q), Q_COPIES more copies per wave bring the Q operand rows
 // of the group's heads into the buffer's Q area: row r (clamped to R - 1) of head hg at
 // [hg][r], LDS chunk c holding global chunk c ^ (r % QCH).
-template <typename G, int POLICY = rows::kStreamPolicy, bool ROPE = false>
+template <typename G, int POLICY = rows::kStreamPolicy, bool ROPE = false, typename RO = RowOffsets>
 __device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& d, bool with_q, char* buf,
-                                           const RowOffsets& ro, int I0 = 0, int I1 = rows::TILE / 4) {
+                                           const RO& ro, int I0 = 0, int I1 = rows::TILE / 4) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int64_t off = int64_t(d.pid < 0 ? 0 : d.pid) * p.page_stride +
@@ -1231,6 +1261,30 @@ __device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& 
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (rows::lds_void*)dst, 16, int(ro.v[i]), 0, 0, POLICY);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (rows::lds_void*)(dst + rows::TILE_BYTES), 16, int(ro.v[i]), 0,
                                                0, POLICY);
+    }
+  } else if constexpr (ROPE && G::P == 1 && G::S == 1) {
+    // Rotary kernel: every lane of copy i reads token T0 + r (lane_src's token is the row), so a
+    // row is one of this call's new tokens or a cached one for the whole wave; each copy picks its
+    // base (the cache run, or the new row of k_new / v_new) with a scalar select and its lane
+    // offset with a vector one, instead of per-lane 64-bit source arithmetic for every copy.
+    const char* kg = uniform_ptr(reinterpret_cast<const char*>(p.k_cache + off));
+    const char* vg = uniform_ptr(reinterpret_cast<const char*>(p.v_cache + off));
+    const int hgl = (lane >> 4) % G::HG;
+    // new row t of the sequence sits at kn0 + t * kn_ss (elements)
+    const uint16_t* kn0 = uniform_ptr(p.k_new + d.b * p.kn_sb + int64_t(d.g * G::HG) * p.kn_sh - d.c * p.kn_ss);
+    const uint16_t* vn0 = uniform_ptr(p.v_new + d.b * p.vn_sb + int64_t(d.g * G::HG) * p.vn_sh - d.c * p.vn_ss);
+    const int64_t lk = 2 * (hgl * p.kn_sh), lv = 2 * (hgl * p.vn_sh);  // bytes
+#pragma unroll
+    for (int i = I0; i < I1; ++i) {
+      const int r = i * 4 + wave;
+      const int t = d.T0 + r;
+      const bool nw = t >= d.c && t < d.L;  // wave-uniform
+      const int64_t cc16 = 16 * ((lane & 15) ^ rows::swz(r));
+      const char* ks = nw ? reinterpret_cast<const char*>(kn0 + t * p.kn_ss) + lk + cc16 : kg + ro.v[i];
+      const char* vs = nw ? reinterpret_cast<const char*>(vn0 + t * p.vn_ss) + lv + cc16 : vg + ro.v[i];
+      __builtin_amdgcn_global_load_lds(ks, (rows::lds_void*)(buf + r * rows::ROW_BYTES), 16, 0, POLICY);
+      __builtin_amdgcn_global_load_lds(vs, (rows::lds_void*)(buf + rows::TILE_BYTES + r * rows::ROW_BYTES), 16, 0,
+                                       POLICY);
     }
   } else {
     const char* kg = uniform_ptr(reinterpret_cast<const char*>(p.k_cache + off));
@@ -1258,14 +1312,18 @@ __device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& 
     for (int i = 0; i < G::Q_COPIES; ++i) {
       const int qi = wave * G::Q_COPIES + i;                      // 1 KiB piece of the Q area
       const int ar = qi * (1024 / G::QROW) + lane / G::QCH;       // area row: head hq_g, query row rr
-      const int hq_g = ar / 16;
       const int row = ar % 16;
-      const int rr = min(row, p.R - 1);
-      const int jq = rr / p.g;
-      const int hq = rr - jq * p.g;
       const int gq = (lane % G::QCH) ^ (row % G::QCH);
-      const uint16_t* src =
-          p.q + d.b * p.q_sb + jq * p.q_ss + ((d.g * G::HG + hq_g) * p.g + hq) * p.q_sh + gq * 8;
+      const uint16_t* src;
+      if constexpr (ROPE) {
+        src = uniform_ptr(p.q + d.b * p.q_sb + int64_t(d.g * G::HG) * p.g * p.q_sh) + ro.q[i];
+      } else {
+        const int hq_g = ar / 16;
+        const int rr = min(row, p.R - 1);
+        const int jq = rr / p.g;
+        const int hq = rr - jq * p.g;
+        src = p.q + d.b * p.q_sb + jq * p.q_ss + ((d.g * G::HG + hq_g) * p.g + hq) * p.q_sh + gq * 8;
+      }
       if (ROPE && row >= p.R && row < p.R + 2 * p.s_q) {
         // rotary: rows R + 2 j and R + 2 j + 1 of every head's area hold the cos and sin rows of
         // position c + j (token j of this call)
@@ -1877,7 +1935,12 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   tile_window<NCH, TOK>(p, st, s, e, T1, win);
   TileDesc dA = tile_desc(win, s);
   TileDesc dB = dA;
-  const RowOffsets ro = row_offsets<G>(p);
+  const auto ro = [&] {
+    if constexpr (kRope)
+      return row_offsets_q<G>(p);
+    else
+      return row_offsets<G>(p);
+  }();
   rows_issue<G, kPolicy, kRope>(p, dA, kQInLds, lds, ro);
   if (n > 1) {
     dB = tile_desc(win, s + 1);
