@@ -2027,17 +2027,20 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     // With phases, a segment end merges the phase states in this buffer first, and tile j + 2's
     // copies wait until that is done.
     const bool defer = G::P > 1 && seg_end;
-    // Tile j + 2's copies go out in two halves, one before and one after tile j's compute: this
-    // wave's copy issue stalls while earlier copies drain, and the split lets that stall overlap
-    // the compute (7B decode 31.0 -> 30.7 us, config-5 verify 77.8 -> 74.5 us per call, against
-    // issuing all of them before the compute).
+    // Verify rows issue tile j + 2's copies in two halves, one before and one after tile j's
+    // compute: the wave's copy issue stalls while earlier copies drain, and the split lets that
+    // stall overlap the longer compute (config-5 verify 60.3 against 66.7 us per call with every
+    // copy first).  Decode rows' compute is short: every row copy goes out first, the Q rows
+    // after the compute (7B decode at B = 8 16.9 against 17.3 us, at B = 32 29.2 against
+    // 29.3-29.4).
+    constexpr int kIssueFirst = NT == 1 ? rows::TILE / 4 : rows::TILE / 8;
     TileDesc d2 = dB;
     const bool next2 = j + 2 < n;
     if (next2) {
       const int x2 = s + j + 2;
       if (__builtin_expect(x2 - win.x0 >= 64, 0)) tile_window<NCH, TOK>(p, st, x2, e, T1, win);
       d2 = tile_desc(win, x2);
-      if (!defer) rows_issue<G, kPolicy, kRope>(p, d2, false, buf, ro, 0, 4);
+      if (!defer) rows_issue<G, kPolicy, kRope>(p, d2, false, buf, ro, 0, kIssueFirst);
     }
     dA = dB;
     dB = d2;
@@ -2053,7 +2056,8 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
           compute_tile<HD, NT, true>(p, tl[sub], T0s, qf, lim, lim_min, m_run, l_run, acc);
       }
     }
-    if (next2 && !defer) rows_issue<G, kPolicy, kRope>(p, d2, q_area_copy<G, kRope>(p, d2, kQInLds), buf, ro, 4, 8);
+    if (next2 && !defer)  // the rest, and the Q rows when tile j + 2 starts a segment
+      rows_issue<G, kPolicy, kRope>(p, d2, q_area_copy<G, kRope>(p, d2, kQInLds), buf, ro, kIssueFirst, rows::TILE / 4);
 
     stores_prev2 = stores_prev;
     stores_prev = 0;
