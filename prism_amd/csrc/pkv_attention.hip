@@ -416,7 +416,7 @@ constexpr int kPrefillDepth = PKV_PREFILL_DEPTH;
 // SPLIT_P feeds P to the PV MFMA as a bf16 hi + lo pair (two MFMAs) instead of one bf16
 // rounding: decode has an order of magnitude of MFMA headroom, and short contexts then keep the
 // output error down to the output's own bf16 rounding.
-template <int HD, int NT, bool SPLIT_P>
+template <int HD, int NT, bool SPLIT_P, bool VT = false>
 __device__ __forceinline__ void compute_tile(const AttnParams& p, const KVTile<HD>& tl, int T0,
                                              const bf16x8 (&qf)[NT][HD / 32], const int (&lim)[NT], int lim_min,
                                              float (&m_run)[NT], float (&l_run)[NT], f32x4 (&acc)[NT][HD / 16]) {
@@ -425,11 +425,15 @@ __device__ __forceinline__ void compute_tile(const AttnParams& p, const KVTile<H
   const int lane = threadIdx.x & 63;
   const int lq = lane >> 4;
 
-  // V^T operands: PV MFMA n covers head-dim elements d = DPL*i + n (i = M row = lane li);
-  // element e of the operand is token T0 + 8lq + e.
+  // V^T operands: PV MFMA n covers head-dim elements d = DPL*i + n (i = M row = lane li), or
+  // with VT the operands rows_read_tile_vt read; element e of the operand is token T0 + 8lq + e.
   bf16x8 vt[DPL];
 #pragma unroll
   for (int n = 0; n < DPL; ++n) {
+    if constexpr (VT) {
+      vt[n] = __builtin_bit_cast(bf16x8, u32x4{tl.vr[n].w[0], tl.vr[n].w[1], tl.vr[n].w[2], tl.vr[n].w[3]});
+      continue;
+    }
     const int w = n >> 1;
     const uint32_t sel = (n & 1) ? 0x07060302u : 0x05040100u;
     u32x4 pk;
@@ -1336,6 +1340,30 @@ __device__ __forceinline__ void rows_issue(const AttnParams& p, const TileDesc& 
   }
 }
 
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((const rows::lds_void*)p));
+}
+
+// LDS transpose reads (ds_read_b64_tr_b16) issued from inline assembly, and their wait.  The
+// compiler's builtin for this instruction makes it wait for every outstanding global-to-LDS copy
+// first (vmcnt(0)), which would drain the copy pipeline of the next tiles on every tile; as
+// assembly the read issues at once.  The compiler does not track these reads: the values must not
+// be touched before lds_tr_wait, which waits for every outstanding LDS access and hands the
+// registers on (its "+v" operands keep every use of them after the wait).
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_read_tr16_issue(uint32_t addr) {
+  u32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+
+__device__ __forceinline__ void lds_tr_wait(u32x2 (&a)[8], u32x2 (&b)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7]),
+                 "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]), "+v"(b[4]), "+v"(b[5]), "+v"(b[6]), "+v"(b[7]));
+}
+
 // MFMA operands of subtile s of wave w's slice of the tile in LDS buffer `buf` (load_tile's
 // register layout); T0s is the subtile's first token, V rows at or past t_end read as zero.
 template <typename G>
@@ -1379,6 +1407,85 @@ __device__ __forceinline__ void rows_read_tile(const char* buf, int w, int s, in
       for (int k = 0; k < G::HD / 32; ++k) tl.vr[e].w[k] = keep ? tl.vr[e].w[k] : 0u;
     }
   }
+}
+
+// The same tile at head_dim 128 with the V^T operands read by LDS transpose reads
+// (ds_read_b64_tr_b16) instead of gathered from V rows by byte permutes.  In each 16-lane group,
+// lane 4 j + c names 4 consecutive elements of row j of a 4 x 16 block and receives column (its
+// index in the group) of the block.  Naming elements 32 c + 4 n .. + 3 of token rows 8 lq + j
+// (then 8 lq + 4 + j) hands lane (li, lq) operand n = head-dim element 32 (li >> 2) + 4 n +
+// (li & 3) over keys 8 lq .. 8 lq + 7, so the PV product leaves element 32 lq + 4 n + r of the
+// lane's row in acc[n][r] (o_elem reads it).  vto[m] is the lane's byte offset in wave slice w of
+// a V tile for operands 2 m and 2 m + 1 (+ 8 B), the same for every tile; the second four rows
+// lie 4 KiB further, under the same swizzle (swz ignores bit 2 of the row).
+template <typename G>
+__device__ __forceinline__ void rows_vt_offsets(int w, uint32_t (&vto)[4]) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15;
+  const int lq = lane >> 4;
+  const int t = 8 * lq + (li >> 2);
+  const int c = li & 3;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) vto[m] = uint32_t(t * rows::ROW_BYTES + (w * 16 + ((4 * c + m) ^ rows::swz(t))) * 16);
+}
+
+template <typename G>
+__device__ __forceinline__ void rows_read_tile_vt(const char* buf, int w, int T0s, int t_end, const uint32_t (&vto)[4],
+                                                  KVTile<G::HD>& tl) {
+  static_assert(G::HD == 128 && G::S == 1, "transpose reads cover one 128-wide head row per LDS row");
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15;
+  const int lq = lane >> 4;
+  constexpr int kHi = 4 * rows::ROW_BYTES;
+  const uint32_t vb = lds_addr(buf + rows::TILE_BYTES);
+  u32x2 lo[8], hi[8];
+  asm volatile("" ::: "memory");  // after this wave's own LDS stores (appended rows)
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t a = vb + vto[m];
+    lo[2 * m] = lds_read_tr16_issue<0>(a);
+    lo[2 * m + 1] = lds_read_tr16_issue<8>(a);
+    hi[2 * m] = lds_read_tr16_issue<kHi>(a);
+    hi[2 * m + 1] = lds_read_tr16_issue<kHi + 8>(a);
+  }
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+    const int r = 8 * (li >> 2) + 4 * a + (li & 3);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int chunk = w * 16 + ((4 * kk + lq) ^ rows::swz(r));
+      tl.kr[a][kk] = *reinterpret_cast<const u32x4*>(buf + r * rows::ROW_BYTES + chunk * 16);
+    }
+  }
+  lds_tr_wait(lo, hi);
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    tl.vr[n].w[0] = lo[n][0];
+    tl.vr[n].w[1] = lo[n][1];
+    tl.vr[n].w[2] = hi[n][0];
+    tl.vr[n].w[3] = hi[n][1];
+  }
+  // keys past the sequence: P = 0 must not meet a stale NaN (word k of an operand holds keys
+  // 8 lq + 2 k and 2 k + 1); only a sequence's last subtile has them
+  if (__builtin_expect(T0s + rows::TILE > t_end, 0)) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int t = T0s + 8 * lq + 2 * k;
+      const uint32_t keep = (t < t_end ? 0x0000FFFFu : 0u) | (t + 1 < t_end ? 0xFFFF0000u : 0u);
+#pragma unroll
+      for (int n = 0; n < 8; ++n) tl.vr[n].w[k] &= keep;
+    }
+  }
+}
+
+// Element 4 DPL lq + DPL r + n of the lane's output row from its accumulators: acc[n][r] with V^T
+// gathered by permutes, acc[2 r + n / 4][n % 4] with V^T from transpose reads (rows_read_tile_vt).
+template <bool VT, int DPL>
+__device__ __forceinline__ float o_elem(const f32x4 (&a)[DPL], int n, int r) {
+  if constexpr (VT)
+    return a[2 * r + (n >> 2)][n & 3];
+  else
+    return a[n][r];
 }
 
 // Chunk ch of row `row` of group head hg's part of the buffer's Q area (stored at chunk
@@ -1570,6 +1677,11 @@ template <int NT>
 __device__ __forceinline__ void compute_tile_prefill(const AttnParams& p, const KVTile<128>& tl, int T0,
                                                      const bf16x8 (&qf)[NT][4], const int (&lim)[NT], int lim_min,
                                                      float (&m_run)[NT], float (&l_run)[NT], f32x4 (&acc)[NT][8]);
+template <int NT>
+__device__ __forceinline__ void compute_tile_prefill_vt(const AttnParams& p, const KVTile<128>& tl, int T0,
+                                                        const bf16x8 (&qf)[NT][4], const int (&lim)[NT], int lim_min,
+                                                        float (&m_run)[NT], float (&l_run)[NT],
+                                                        f32x4 (&acc)[NT][8]);
 
 // ---- split-K partials of decode_lean_kernel, merged inside the launch ----
 // For the in-launch merge, partials are written and read with the sc1 cache policy:
@@ -1907,6 +2019,9 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   constexpr int kQCopies = kQInLds ? G::Q_COPIES : 0;
   constexpr int BUF = 2 * rows::TILE_BYTES + (kQInLds ? G::Q_BYTES : 0);  // K tile | V tile | Q
   constexpr int kPolicy = NT == 1 || CASCADE_SUFFIX ? rows::kStreamPolicy : rows::kVerifyPolicy;
+  // V^T operands by LDS transpose reads at head_dim 128 (config-5 verify 58.1-58.2 against
+  // 60.2-60.3 us per call with byte permutes, 7B decode at B = 8 16.3 against 16.4-16.5)
+  constexpr bool kVTr = HD == 128;
   __shared__ __attribute__((aligned(16))) char lds[2 * BUF];
 
   const int lane = threadIdx.x & 63;
@@ -1947,6 +2062,8 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     rows_issue<G, kPolicy, kRope>(p, dB, q_area_copy<G, kRope>(p, dB, kQInLds), lds + BUF, ro);
   }
 
+  uint32_t vto[4];
+  if constexpr (kVTr) rows_vt_offsets<G>(w, vto);
   bf16x8 qf[NT][KK];
   int lim[NT];
   int lim_min = 0x7fffffff;
@@ -2018,9 +2135,13 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
       rows_append_from_lds<G>(p, d, buf);
     }
     KVTile<HD> tl[G::S];
+    if constexpr (kVTr) {
+      rows_read_tile_vt<G>(buf, w, d.T0 + rows::TILE * ph, d.L, vto, tl[0]);
+    } else {
 #pragma unroll
-    for (int sub = 0; sub < G::S; ++sub)
-      rows_read_tile<G>(buf, w, sub, d.T0 + rows::TILE * (ph * G::S + sub), d.L, tl[sub]);
+      for (int sub = 0; sub < G::S; ++sub)
+        rows_read_tile<G>(buf, w, sub, d.T0 + rows::TILE * (ph * G::S + sub), d.L, tl[sub]);
+    }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
     raw_barrier();                       // nobody reads this buffer any more
     const bool seg_end = !(j + 1 < n && d.T0 + TOK < d.L);
@@ -2050,10 +2171,12 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
       if (T0s < d.L) {
         // verify: the prefill kernel's ILP-ordered tile update (all QK products, then the softmax
         // of every N tile, then every PV product)
-        if constexpr (NT > 1 && HD == 128)
+        if constexpr (NT > 1 && kVTr)
+          compute_tile_prefill_vt<NT>(p, tl[sub], T0s, qf, lim, lim_min, m_run, l_run, acc);
+        else if constexpr (NT > 1 && HD == 128)
           compute_tile_prefill<NT>(p, tl[sub], T0s, qf, lim, lim_min, m_run, l_run, acc);
         else
-          compute_tile<HD, NT, true>(p, tl[sub], T0s, qf, lim, lim_min, m_run, l_run, acc);
+          compute_tile<HD, NT, true, kVTr>(p, tl[sub], T0s, qf, lim, lim_min, m_run, l_run, acc);
       }
     }
     if (next2 && !defer)  // the rest, and the Q rows when tile j + 2 starts a segment
@@ -2093,7 +2216,9 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
             if constexpr (DPL == 8) {
               u32x4 ov;
 #pragma unroll
-              for (int k = 0; k < 4; ++k) ov[k] = pack_bf16x2(acc[nt][2 * k][r] * inv, acc[nt][2 * k + 1][r] * inv);
+              for (int k = 0; k < 4; ++k)
+                ov[k] = pack_bf16x2(o_elem<kVTr, DPL>(acc[nt], 2 * k, r) * inv,
+                                    o_elem<kVTr, DPL>(acc[nt], 2 * k + 1, r) * inv);
               st16(dst + DPL * r, ov);
             } else {
               u32x2 ov;
@@ -2131,7 +2256,8 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
           for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int k = 0; k < DPL / 2; ++k) {
-              const float lo = acc[nt][2 * k][r] * inv, hi = acc[nt][2 * k + 1][r] * inv;
+              const float lo = o_elem<kVTr, DPL>(acc[nt], 2 * k, r) * inv;
+              const float hi = o_elem<kVTr, DPL>(acc[nt], 2 * k + 1, r) * inv;
               ovf |= f16_overflows(lo, hi);
               ov[r][k] = pack_f16x2(lo, hi);
             }
@@ -2320,30 +2446,6 @@ constexpr int BUF = 2 * KV_BYTES;      // K | V
 __device__ __forceinline__ int swz_v(int r) { return ((r & 3) << 1) | (((r >> 3) & 1) << 3); }
 }  // namespace pf
 
-// LDS byte address of a pointer into a __shared__ array.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return uint32_t(reinterpret_cast<uintptr_t>((const rows::lds_void*)p));
-}
-
-// LDS transpose reads (ds_read_b64_tr_b16) issued from inline assembly, and their wait.  The
-// compiler's builtin for this instruction makes it wait for every outstanding global-to-LDS copy
-// first (vmcnt(0)), which would drain the copy pipeline of the next tiles on every tile; as
-// assembly the read issues at once.  The compiler does not track these reads: the values must not
-// be touched before lds_tr_wait, which waits for every outstanding LDS access and hands the
-// registers on (its "+v" operands keep every use of them after the wait).
-template <int OFF>
-__device__ __forceinline__ u32x2 lds_read_tr16_issue(uint32_t addr) {
-  u32x2 r;
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
-  return r;
-}
-
-__device__ __forceinline__ void lds_tr_wait(u32x2 (&a)[8], u32x2 (&b)[8]) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7]),
-                 "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]), "+v"(b[4]), "+v"(b[5]), "+v"(b[6]), "+v"(b[7]));
-}
-
 template <int OPS, int NBUF>
 __device__ __forceinline__ void pf_wait(int ahead) {
   // at most `ahead` later tiles' copies (OPS per tile for this wave) may stay in flight
@@ -2509,6 +2611,20 @@ __device__ __forceinline__ void compute_tile_prefill(const AttnParams& p, const 
       for (int pp = 0; pp < 4; ++pp) pk[pp] = __builtin_amdgcn_perm(tl.vr[2 * pp + 1].w[w], tl.vr[2 * pp].w[w], sel);
       vt[n] = __builtin_bit_cast(bf16x8, pk);
     }
+  };
+  compute_tile_prefill_ops<NT>(p, tl.kr, [] {}, v_ops, T0, qf, lim, lim_min, m_run, l_run, acc);
+}
+
+// The same update on a tile whose V^T operands came from transpose reads (rows_read_tile_vt).
+template <int NT>
+__device__ __forceinline__ void compute_tile_prefill_vt(const AttnParams& p, const KVTile<128>& tl, int T0,
+                                                        const bf16x8 (&qf)[NT][4], const int (&lim)[NT], int lim_min,
+                                                        float (&m_run)[NT], float (&l_run)[NT],
+                                                        f32x4 (&acc)[NT][8]) {
+  auto v_ops = [&](bf16x8 (&vt)[8]) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+      vt[n] = __builtin_bit_cast(bf16x8, u32x4{tl.vr[n].w[0], tl.vr[n].w[1], tl.vr[n].w[2], tl.vr[n].w[3]});
   };
   compute_tile_prefill_ops<NT>(p, tl.kr, [] {}, v_ops, T0, qf, lim, lim_min, m_run, l_run, acc);
 }

@@ -1,4 +1,5 @@
-"""The prefill kernel issues its LDS transpose reads (ds_read_b64_tr_b16) from inline assembly, so
+"""The prefill and balanced decode / verify kernels issue their LDS transpose reads
+(ds_read_b64_tr_b16) from inline assembly, so
 the compiler neither waits for them nor knows that their destination registers are still being
 written until the explicit `s_waitcnt lgkmcnt(0)` that follows.  This test compiles
 pkv_attention.hip for gfx950 to assembly and checks, for every such read in every kernel, that no
