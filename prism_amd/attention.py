@@ -177,9 +177,10 @@ def append_kv(k_cache, v_cache, k, v, cache_seqlens, block_table, *, status=None
 
 
 # Cascade attention is taken by itself (shared_prefix_tokens=None) from this many shared keys and
-# sequences on: at the Qwen2.5-7B verify shape (64 sequences, 5 query rows) it is on par with the
-# ordinary call at a 1792-key shared prefix (61.2 vs 62.2 us per layer) and 1.9x faster at 7936.
-AUTO_CASCADE_MIN_TOKENS = 1024
+# sequences on: at the Qwen2.5-7B verify shape (64 sequences, 5 query rows) the ordinary call is
+# faster at a 1792-key shared prefix (58.1-58.2 vs 59.8-60.7 us per layer) and the cascade 1.9x
+# faster at 7936; interpolated, the two cross near 2.2k shared keys.
+AUTO_CASCADE_MIN_TOKENS = 2048
 AUTO_CASCADE_MIN_BATCH = 4
 
 

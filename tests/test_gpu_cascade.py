@@ -132,8 +132,8 @@ def test_cascade_without_append_checks_row_visibility(gpu):
 
 
 def test_cascade_chosen_from_the_block_table_of_forked_branches(gpu):
-    # a verify batch of 8 branches forked from one 2000-token prompt, each grown by its own suffix
-    # (the boundary page copied on write): build_block_table records the 7 shared full pages and
+    # a verify batch of 8 branches forked from one 2400-token prompt, each grown by its own suffix
+    # (the boundary page copied on write): build_block_table records the 9 shared full pages and
     # flash_attn_with_kvcache, called exactly as the reference calls it (no shared-prefix
     # argument), takes cascade attention; results match the oracle and the ordinary path
     from prism_amd import shared_prefix_of
@@ -143,8 +143,8 @@ def test_cascade_chosen_from_the_block_table_of_forked_branches(gpu):
     kv.k_pool.copy_(torch.randn(kv.k_pool.shape, generator=g).to(torch.bfloat16))
     kv.v_pool.copy_(torch.randn(kv.v_pool.shape, generator=g).to(torch.bfloat16))
     kv.new_sequence(0)
-    kv._ensure_capacity(0, 2000)
-    kv.seq_len[0] = 2000
+    kv._ensure_capacity(0, 2400)
+    kv.seq_len[0] = 2400
     ids = list(range(8))
     for sid in ids[1:]:
         kv.fork_sequence(0, sid)
@@ -154,13 +154,14 @@ def test_cascade_chosen_from_the_block_table_of_forked_branches(gpu):
         kv.update_seqlens([sid], grow)
     kv.prepare_append(ids, s_q)
     bt, sl = kv.build_block_table(ids)
-    assert shared_prefix_of(bt, sl) == 7 * P
+    assert shared_prefix_of(bt, sl) == 9 * P
+    assert 9 * P >= prism_amd.attention.AUTO_CASCADE_MIN_TOKENS
     q = torch.randn(len(ids), s_q, nh, hd, generator=g).to(torch.bfloat16)
     k = torch.randn(len(ids), s_q, n_kv, hd, generator=g).to(torch.bfloat16)
     v = torch.randn(len(ids), s_q, n_kv, hd, generator=g).to(torch.bfloat16)
     kc_cpu, vc_cpu = kv.k_caches[0].cpu(), kv.v_caches[0].cpu()
     kc0, vc0 = kv.k_caches[0].clone(), kv.v_caches[0].clone()
-    print(f"auto cascade B={len(ids)} shared={7 * P} s_q={s_q}", flush=True)
+    print(f"auto cascade B={len(ids)} shared={9 * P} s_q={s_q}", flush=True)
     out = prism_amd.flash_attn_with_kvcache(q.to(gpu), kv.k_caches[0], kv.v_caches[0], k.to(gpu), v.to(gpu),
                                             cache_seqlens=sl, block_table=bt, causal=True)
     torch.cuda.synchronize()
