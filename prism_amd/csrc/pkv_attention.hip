@@ -19,7 +19,9 @@
 // PV MFMA wants, and all softmax statistics of a lane's row live in that lane, so the
 // online-softmax rescale of O needs no cross-lane traffic; only the tile max is reduced across
 // the four 16-lane groups.  V rows arrive head_dim-contiguous: each lane loads 8 tokens x
-// head_dim/16 elements and transposes them with byte permutes into the token-major V^T operand.
+// head_dim/16 elements and transposes them with byte permutes into the token-major V^T operand,
+// except where a kernel stages V tiles in LDS at head_dim 128: there LDS transpose reads
+// (ds_read_b64_tr_b16) deliver the operand directly.
 // Every K/V byte of a (sequence, KV head) is fetched once per query-row tile.
 #include <math.h>
 
