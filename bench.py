@@ -588,7 +588,8 @@ def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build runs on a single MI355X and has no multi-GPU "
-              "path (the paged KV hot path shards by KV head / sequence; see DESIGN.md). Use --gpus 1.",
+              "path (the paged KV hot path would shard by KV head, each rank running its heads' "
+              "shard of every call unchanged). Use --gpus 1.",
               file=sys.stderr)
         return 2
     import torch
