@@ -54,7 +54,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--workload", choices=["config2", "config3", "config4", "config5", "decode-14B", "decode-0.5B",
-                                           "decode-7B-tp4", "epilogue", "tables", "peak"], default="config3")
+                                           "decode-7B-tp4", "long-decode", "long-decode-b1", "prefill-4096",
+                                           "epilogue", "tables", "peak"], default="config3")
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = library choice)")
     ap.add_argument("--grid", type=int, default=0, help="workgroups of the balanced kernel (0 = one per CU)")
     ap.add_argument("--layers", type=int, default=0, help="layers (0 = the model's)")
@@ -677,6 +678,11 @@ def main() -> int:
     print(f"[bench] building {args.workload} workload (seed={args.seed})", file=sys.stderr, flush=True)
     if args.workload.startswith("decode-"):
         w = workloads.ragged_decode(args.workload[len("decode-"):], dev, seed=args.seed, layers=args.layers or None)
+    elif args.workload.startswith("long-decode"):
+        w = workloads.long_decode(dev, seed=args.seed, layers=args.layers or None,
+                                  batch=1 if args.workload.endswith("-b1") else 32)
+    elif args.workload == "prefill-4096":
+        w = workloads.prompt_prefill(dev, seed=args.seed, layers=args.layers or None, prompt=4096)
     else:
         w = getattr(workloads, args.workload)(dev, seed=args.seed, layers=args.layers or None)
     L = w.layers
@@ -723,12 +729,19 @@ def main() -> int:
            "sum_ctx": int(w.ctx.sum()), "max_ctx": int(w.ctx.max()), "seed": args.seed,
            "split_tokens": args.split or "auto", "grid": args.grid or "auto", "merge": args.merge}
     per_call = f"HIP events around K graph replays of the {L}-call step, per call = step / {L}"
-    if args.workload in ("config2", "config3") or args.workload.startswith("decode-"):
+    decode_like = args.workload in ("config2", "config3") or args.workload.startswith(("decode-", "long-decode"))
+    if decode_like:
         traffic, traffic_src = profiled_traffic(args, w)
         if args.workload == "config3":
             metric = "paged decode attn HBM GB/s (% of peak) + us/step, Qwen2.5-7B shape b=32"
             cfg["workload"] = ("config3: Qwen2.5-7B paged decode (append + attention), 28 layers, b=32, ctx "
                                "lognormal(1500, 1) in [16, 32768], 2043-page 30 GB pool, 40% churn")
+        elif args.workload.startswith("long-decode"):
+            metric = f"paged decode attn HBM GB/s (% of peak) + us/step, Qwen2.5-7B shape b={w.batch}, long contexts"
+            cfg["workload"] = (f"{args.workload}: " + (
+                "config3's ragged batch (b=32, ctx lognormal(1500, 1), 40% churn) with sequence 0 at 32767 cached "
+                "keys and sequence 1 at 12000" if w.batch > 1 else "one sequence at 32767 cached keys (the B = 1 "
+                "decode graph)") + f", Qwen2.5-7B shape, {L} layers, {kv.max_pages}-page pool")
         elif args.workload.startswith("decode-"):
             shape = w.meta["shape"]
             metric = f"paged decode attn HBM GB/s (% of peak) + us/step, Qwen2.5-{shape} shape b={w.batch}"
@@ -750,11 +763,18 @@ def main() -> int:
             },
         }
         unit = "GB/s"
-    elif args.workload == "config4":
-        cfg["workload"] = ("config4: Qwen2.5-14B varlen chunked prefill over paged KV, 48 layers, b=8 chunks of "
-                           "512 appended onto prefixes ~U{0..4096}, causal, 596-page 30 GB pool")
+    elif args.workload in ("config4", "prefill-4096"):
+        if args.workload == "config4":
+            cfg["workload"] = ("config4: Qwen2.5-14B varlen chunked prefill over paged KV, 48 layers, b=8 chunks of "
+                               "512 appended onto prefixes ~U{0..4096}, causal, 596-page 30 GB pool")
+            metric = "chunked prefill attn TFLOP/s (% of bf16 MFMA peak), Qwen2.5-14B shape b=8 chunk 512"
+        else:
+            cfg["workload"] = ("prefill-4096: Qwen2.5-7B whole-prompt prefill (engine/executor.py:97-120), b=1, a "
+                               f"4096-token prompt with no prefix appended and attended causally, {L} layers, "
+                               f"{kv.max_pages}-page 30 GB pool")
+            metric = "whole-prompt prefill attn TFLOP/s (% of bf16 MFMA peak), Qwen2.5-7B shape b=1 prompt 4096"
         result = {
-            "metric": "chunked prefill attn TFLOP/s (% of bf16 MFMA peak), Qwen2.5-14B shape b=8 chunk 512",
+            "metric": metric,
             "value": round(flops_layer * L / (step_ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", **common,
             "config": cfg,
             "roofline": {

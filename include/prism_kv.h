@@ -16,8 +16,11 @@
  *
  * Conventions shared by every entry point:
  *   - All tensors are device pointers owned by the caller.  Nothing here allocates device
- *     memory, synchronises the host, or touches global mutable state, so every call can be
- *     captured in a HIP graph.  Work is enqueued on `stream` (a hipStream_t; NULL = default).
+ *     memory or synchronises the host, so every call can be captured in a HIP graph.  The one
+ *     piece of global mutable state is the static split-K scratch of pkv_decode_attn_noalloc
+ *     (one array per GPU, shared by every noalloc call on it); every other entry point touches
+ *     only the memory its arguments name.  Work is enqueued on `stream` (a hipStream_t; NULL =
+ *     default).
  *   - K/V element type is bf16 (passed as raw 16-bit words).  A paged cache is laid out
  *     [num_pages, page_size, n_kv, head_dim] with the last three dims contiguous
  *     (engine/kv_cache.py:37-46); `*_page_stride` is the element distance between pages.
@@ -58,8 +61,12 @@ extern "C" {
                                       fp16's range: |V| >= 65520 somewhere; that output is inf.
                                       PKV_DECODE_HEADS keeps fp32 partials */
 #define PKV_STATUS_MERGE_TIMEOUT 16 /* an in-launch merge (PKV_DECODE_FUSED_MERGE) waited past its
-                                       bound for a sequence's split-K parts; that output is stale.
-                                       Never expected: it reports a broken arrival count */
+                                       bound for a sequence's split-K parts, or found its arrival
+                                       counter left over from such a call; that output is stale.
+                                       Never expected: it reports a broken arrival count.  The
+                                       workspace's counter region (its first 64 KiB) is then no
+                                       longer zero: clear it, or pass PKV_DECODE_RESET_COUNTERS
+                                       once, before the next call that uses it */
 
 /* pkv_decode_attn flags (0 = the library's choice of kernel and merge) */
 #define PKV_DECODE_TWO_PASS 1    /* merge split-K partials in a second launch */
@@ -67,6 +74,9 @@ extern "C" {
                                     the last split to finish; balanced kernel with <= 16 query rows
                                     per KV head: merge workgroups appended to its grid) */
 #define PKV_DECODE_HEADS 4       /* use the per-head kernel where the balanced one would run */
+#define PKV_DECODE_RESET_COUNTERS 8 /* clear the workspace's (noalloc: the static scratch's) split-K
+                                       arrival counters before the call: the recovery after
+                                       PKV_STATUS_MERGE_TIMEOUT */
 #define PKV_DECODE_GRID(n) ((int32_t)(n) << 8) /* balanced kernel on n (1..65535) workgroups, not one per CU */
 
 /* ABI version of the loaded library (PKV_ABI_VERSION it was built with). */
@@ -332,6 +342,15 @@ int pkv_silu_mul(const void* gate, int64_t g_stride, const void* up, int64_t u_s
 int pkv_table_update(const int32_t* packet, int32_t n_len, int32_t n_ent, int32_t* block_table,
                      int64_t bt_stride, int32_t* cache_seqlens, int32_t rows, int32_t cols,
                      int32_t num_pages, int32_t* status, void* stream);
+
+/*
+ * Asynchronous read of a status word: one atomic exchange on `stream` moves its bits to *dst (a
+ * device int32) and leaves it 0, so bits that a kernel on another stream sets at the same time
+ * are never lost between a read and a clear.  No counterpart in the reference (flash_attn has no
+ * status word); it lets a host poll the word at the points it already passes through (a copy of
+ * *dst to pinned memory and an event, no synchronisation) instead of after every call.
+ */
+int pkv_status_take(int32_t* status, int32_t* dst, void* stream);
 
 #ifdef __cplusplus
 }

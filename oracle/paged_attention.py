@@ -113,25 +113,29 @@ def gather_seq(cache_bits: np.ndarray, block_table_row: np.ndarray, L: int) -> n
 
 
 def attention_fp64(q_bits: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, block_table: np.ndarray,
-                   seqlens_k: np.ndarray, causal: bool, softmax_scale: float | None = None) -> np.ndarray:
+                   seqlens_k: np.ndarray, causal: bool, softmax_scale: float | None = None,
+                   rows: np.ndarray | None = None) -> np.ndarray:
     """fp64 paged attention. q [B, s_q, nh, hd] bits; caches [pages, P, n_kv, hd] bits.
 
     seqlens_k[b] is the number of keys of sequence b (after any append).  Returns fp64
-    [B, s_q, nh, hd]; rows with no visible key are 0.
+    [B, s_q, nh, hd]; rows with no visible key are 0.  With `rows` (sorted query positions),
+    only those rows are computed and the result is [B, len(rows), nh, hd] (a long prefill chunk
+    checked on a sample of its rows; the causal mask still counts every row's true position).
     """
     B, s_q, nh, hd = q_bits.shape
     n_kv = k_bits.shape[2]
     g = nh // n_kv
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(hd)
-    out = np.zeros((B, s_q, nh, hd), dtype=np.float64)
+    sel = np.arange(s_q) if rows is None else np.asarray(rows, dtype=np.int64)
+    out = np.zeros((B, len(sel), nh, hd), dtype=np.float64)
     for b in range(B):
         L = int(seqlens_k[b])
         if L <= 0:
             continue
         K = bits_to_f64(gather_seq(k_bits, block_table[b], L))  # [L, n_kv, hd]
         V = bits_to_f64(gather_seq(v_bits, block_table[b], L))
-        Q = bits_to_f64(q_bits[b])                              # [s_q, nh, hd]
-        vis = causal_visible(s_q, L) if causal else np.ones((s_q, L), dtype=bool)
+        Q = bits_to_f64(q_bits[b][sel])                         # [rows, nh, hd]
+        vis = (causal_visible(s_q, L) if causal else np.ones((s_q, L), dtype=bool))[sel]
         for h in range(nh):
             kvh = h // g
             s = (Q[:, h, :] @ K[:, kvh, :].T) * scale          # [s_q, L]

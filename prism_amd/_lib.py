@@ -26,6 +26,7 @@ PKV_STATUS_MERGE_TIMEOUT = 16
 PKV_DECODE_TWO_PASS = 1
 PKV_DECODE_FUSED_MERGE = 2
 PKV_DECODE_HEADS = 4
+PKV_DECODE_RESET_COUNTERS = 8
 ABI_VERSION = 1
 
 _I64 = c_int64
@@ -130,6 +131,7 @@ _SIGNATURES = {
     ]),
     "pkv_silu_mul": (c_int32, [_P, _I64, _P, _I64, _P, _I64, _I64, _I32, _P]),
     "pkv_table_update": (c_int32, [_P, _I32, _I32, _P, _I64, _P, _I32, _I32, _I32, _P, _P]),
+    "pkv_status_take": (c_int32, [_P, _P, _P]),           # status, dst, stream
     "pkv_cascade_workspace_bytes": (c_size_t, [_I32] * 8),
     "pkv_cascade_attn": (c_int32, [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64,
                                    _P, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _P, c_size_t,

@@ -33,8 +33,10 @@ from . import _lib
 _BF16 = torch.bfloat16
 _ws_lock = threading.Lock()
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
-_retired: list[torch.Tensor] = []   # outgrown workspaces, kept alive for graphs that captured them
+_captured: set[int] = set()         # data_ptr of every workspace handed to a call under graph capture
+_retired: list[torch.Tensor] = []   # outgrown workspaces a captured graph may still use
 _status: dict[int, torch.Tensor] = {}
+_STATUS_NAMES = {1: "BAD_PAGE", 2: "BAD_POSITION", 4: "SHARED_PREFIX", 8: "PARTIAL_RANGE", 16: "MERGE_TIMEOUT"}
 
 
 def _stream_ptr(device: torch.device) -> int:
@@ -57,13 +59,127 @@ def status_tensor(device: torch.device) -> torch.Tensor:
     return t
 
 
+def _dev_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
+class PrismKVStatusError(RuntimeError):
+    """A kernel flagged an error bit in the device status word (PKV_STATUS_*): an output or a
+    page write of some earlier call was skipped or is not to be trusted.  Raised at a host point
+    the caller already passes through (FlashAttnKVCache.build_block_table / update_seqlens,
+    DecodeBatch.step), a step or two after the call that set it."""
+
+    def __init__(self, bits: int, device: int):
+        names = [n for b, n in _STATUS_NAMES.items() if bits & b] or [hex(bits)]
+        super().__init__(f"prism_amd kernel status on cuda:{device}: {'|'.join(names)} ({bits}) "
+                         "(see PKV_STATUS_* in include/prism_kv.h)")
+        self.bits = bits
+
+
+class _StatusCopies:
+    """Asynchronous reads of one device's status word: pkv_status_take moves the bits into a
+    device slot (atomic exchange with 0), a non-blocking copy brings the slot to pinned host
+    memory, and an event says when it has landed.  Nothing on the host waits."""
+
+    SLOTS = 4
+
+    def __init__(self, device: torch.device):
+        self.dev_slots = torch.zeros(self.SLOTS, dtype=torch.int32, device=device)
+        self.host = torch.zeros(self.SLOTS, dtype=torch.int32, pin_memory=True)
+        self.free = list(range(self.SLOTS))
+        self.pending: list[tuple[torch.cuda.Event, int]] = []
+        self.bits = 0   # landed on the host and not reported yet
+
+    def collect(self, wait: bool) -> None:
+        keep = []
+        for ev, slot in self.pending:
+            if wait:
+                ev.synchronize()
+            if wait or ev.query():
+                self.bits |= int(self.host[slot])
+                self.free.append(slot)
+            else:
+                keep.append((ev, slot))
+        self.pending = keep
+
+    def take(self, device: torch.device, status: torch.Tensor) -> None:
+        if not self.free:
+            return
+        slot = self.free.pop()
+        stream = torch.cuda.current_stream(device)
+        rc = _lib.load().pkv_status_take(status.data_ptr(), self.dev_slots[slot:].data_ptr(), stream.cuda_stream)
+        _lib.check(rc, "pkv_status_take")
+        self.host[slot:slot + 1].copy_(self.dev_slots[slot:slot + 1], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        self.pending.append((ev, slot))
+
+
+_monitors: dict[int, _StatusCopies] = {}
+_checks_enabled = True
+_reset_counters: set[int] = set()   # devices whose noalloc scratch counters need clearing
+
+
+def set_status_checks(enabled: bool) -> None:
+    """Turn the status polls at build_block_table / update_seqlens / DecodeBatch.step on (the
+    default) or off."""
+    global _checks_enabled
+    _checks_enabled = bool(enabled)
+
+
+def _recover(idx: int, bits: int) -> None:
+    """After PKV_STATUS_MERGE_TIMEOUT the split-K arrival counters of this device's workspaces may
+    no longer be zero: clear them (stream-ordered) and have the next noalloc call clear the
+    library's static scratch (PKV_DECODE_RESET_COUNTERS)."""
+    if not bits & _lib.PKV_STATUS_MERGE_TIMEOUT:
+        return
+    with _ws_lock:
+        for (d, _), ws in _workspaces.items():
+            if d == idx:
+                ws[:65536].zero_()
+    _reset_counters.add(idx)
+
+
+def poll_status(device: torch.device | str = "cuda", raise_on_error: bool = True) -> int:
+    """Non-blocking status check for a host point the caller passes through every step: collect
+    the reads that have landed, start a new one (pkv_status_take on the current stream), and,
+    when some landed read holds error bits, raise PrismKVStatusError (or return the bits with
+    raise_on_error=False).  A bit set by a call is seen one or two polls later.  Nothing happens
+    under HIP graph capture or with set_status_checks(False)."""
+    device = torch.device(device)
+    if not _checks_enabled or device.type != "cuda" or torch.cuda.is_current_stream_capturing():
+        return 0
+    idx = _dev_index(device)
+    mon = _monitors.get(idx)
+    if mon is None:
+        mon = _monitors[idx] = _StatusCopies(device)
+    mon.collect(wait=False)
+    mon.take(device, status_tensor(device))
+    bits, mon.bits = mon.bits, 0
+    if bits:
+        _recover(idx, bits)
+        if raise_on_error:
+            raise PrismKVStatusError(bits, idx)
+    return bits
+
+
 def read_status(device: torch.device | str = "cuda", clear: bool = True) -> int:
-    """Synchronously read (and by default clear) the device status word."""
+    """Synchronously read (and by default clear) the device status word, together with any bits
+    an earlier poll_status moved to the host and has not reported yet."""
     device = torch.device(device)
     t = status_tensor(device)
-    v = int(t.item())
+    idx = _dev_index(device)
+    mon = _monitors.get(idx)
+    pending = 0
+    if mon is not None:
+        mon.collect(wait=True)
+        pending = mon.bits
+        if clear:
+            mon.bits = 0
+    v = int(t.item()) | pending
     if clear:
         t.zero_()
+        _recover(idx, v)
     return v
 
 
@@ -77,17 +193,21 @@ def _workspace(device: torch.device, nbytes: int, stream: int, allow_static: boo
     replays and the eager calls then share it, which is safe because Prism issues both from one
     thread in order.  With allow_static, a capture that finds no sized workspace gets None: the
     decode call then runs pkv_decode_attn_noalloc, whose scratch is the library's static device
-    array.  A workspace that grows is retired, never freed: a captured graph may still hold its
-    address."""
+    array.  A workspace that grows is dropped (the caching allocator reuses its memory) unless a
+    call under graph capture was handed it: a captured graph keeps its address, so such a
+    workspace is retired instead, kept alive for the rest of the process."""
     if nbytes == 0:
         return None
-    idx = device.index if device.index is not None else torch.cuda.current_device()
+    idx = _dev_index(device)
     key = (idx, stream)
+    capturing = torch.cuda.is_current_stream_capturing()
     with _ws_lock:
         ws = _workspaces.get(key)
         if ws is not None and ws.numel() >= nbytes:
+            if capturing:
+                _captured.add(ws.data_ptr())
             return ws
-        if torch.cuda.is_current_stream_capturing():
+        if capturing:
             sized = [t for (d, _), t in _workspaces.items() if d == idx and t.numel() >= nbytes]
             if not sized:
                 if allow_static:
@@ -96,12 +216,14 @@ def _workspace(device: torch.device, nbytes: int, stream: int, allow_static: boo
                     f"split-K workspace of {nbytes} bytes must be sized by an eager call on this device "
                     "before HIP graph capture")
             ws = max(sized, key=lambda t: t.numel())
+            _captured.add(ws.data_ptr())
         else:
             ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         old = _workspaces.get(key)
-        if old is not None:
-            _retired.append(old)
         _workspaces[key] = ws
+        if old is not None and old.data_ptr() in _captured and \
+                all(t.data_ptr() != old.data_ptr() for t in _workspaces.values()):
+            _retired.append(old)
         return ws
 
 
@@ -184,22 +306,31 @@ AUTO_CASCADE_MIN_TOKENS = 2048
 AUTO_CASCADE_MIN_BATCH = 4
 
 
-def shared_prefix_of(block_table: torch.Tensor, cache_seqlens) -> int:
+def shared_prefix_of(block_table: torch.Tensor, cache_seqlens, *, s_q: int = 1, causal: bool = True,
+                     appends: bool = True, page_size: int | None = None) -> int:
     """Keys every sequence of the batch shares, as FlashAttnKVCache.build_block_table recorded
     them for this block_table (identical leading pages that every sequence fills); 0 when the
     table did not come from there, when either tensor has been written since (torch's version
     counters), when cache_seqlens is not the tensor built with it, or under HIP graph capture
-    (a captured launch would keep the prefix for every replay)."""
+    (a captured launch would keep the prefix for every replay).
+
+    Cascade attention gives every query row the whole prefix.  Without an append, a causal call
+    with s_q > 1 lets query row 0 see only keys t <= min(cache_seqlens) - s_q, so the prefix is
+    cut to the whole pages below that bound (page_size: the cache's)."""
     meta = getattr(block_table, "_pkv_shared_prefix", None)
     if not meta or not isinstance(cache_seqlens, torch.Tensor):
         return 0
-    tokens, bt_version, sl_ptr, sl_version = meta
+    tokens, bt_version, sl_ptr, sl_version, sl_min = meta
     if tokens <= 0 or block_table._version != bt_version:
         return 0
     if cache_seqlens.data_ptr() != sl_ptr or cache_seqlens._version != sl_version:
         return 0
     if block_table.is_cuda and torch.cuda.is_current_stream_capturing():
         return 0
+    if causal and not appends and s_q > 1:
+        seen = sl_min - s_q + 1            # keys row 0 sees in the shortest sequence
+        P = int(page_size) if page_size else 1
+        tokens = min(tokens, max(seen, 0) // P * P)
     return int(tokens)
 
 
@@ -316,8 +447,11 @@ def flash_attn_with_kvcache(
     stream = _stream_ptr(device)
     g = n_heads // n_kv
     if shared_prefix_tokens is None:
-        auto = shared_prefix_of(block_table, cache_seqlens)
+        auto = shared_prefix_of(block_table, cache_seqlens, s_q=s_q, causal=causal, appends=k is not None,
+                                page_size=page_size)
         shared_prefix_tokens = auto if auto >= AUTO_CASCADE_MIN_TOKENS and batch >= AUTO_CASCADE_MIN_BATCH else 0
+    if noalloc:
+        shared_prefix_tokens = 0   # the cascade needs a workspace of this module's
     if s_q * g <= 64:
         if num_splits and num_splits > 0 and not split_tokens:
             per_split = -(-(max_blocks * page_size) // num_splits)
@@ -342,15 +476,22 @@ def flash_attn_with_kvcache(
             nbytes = max(nbytes, 65536 + 2 * int(grid) * 4 * s_q * g * 260)
         ws = None if noalloc else _workspace(device, nbytes, stream, allow_static=True)
         if noalloc or (ws is None and nbytes > 0):
+            idx = _dev_index(device)
+            flags = _decode_flags(two_pass, kernel, grid)
+            reset = idx in _reset_counters and not torch.cuda.is_current_stream_capturing()
+            if reset:   # after a merge timeout: clear the static scratch's counters first
+                flags |= _lib.PKV_DECODE_RESET_COUNTERS
             rc = lib.pkv_decode_attn_noalloc(
                 q.data_ptr(), *qs, kp, *ks, vp, *vs,
                 k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0),
                 block_table.data_ptr(), block_table.stride(0), cache_seqlens.data_ptr(),
                 out.data_ptr(), *os_,
                 batch, s_q, n_heads, n_kv, hd, page_size, num_pages, max_blocks,
-                1 if causal else 0, scale, int(split_tokens), _decode_flags(two_pass, kernel, grid),
+                1 if causal else 0, scale, int(split_tokens), flags,
                 st.data_ptr(), stream)
             _lib.check(rc, "pkv_decode_attn_noalloc")
+            if reset:
+                _reset_counters.discard(idx)
             return out
         rc = lib.pkv_decode_attn(
             q.data_ptr(), *qs, kp, *ks, vp, *vs,

@@ -1929,11 +1929,15 @@ __device__ __forceinline__ void merge_workgroup(const AttnParams& p, const SeqTa
       if ((seen & 0xffff) >= sp.np) break;
       __builtin_amdgcn_s_sleep(4);
     }
-    *ready_s = (seen & 0xffff) >= sp.np;
-    if (!*ready_s) flag_status(p.status, PKV_STATUS_MERGE_TIMEOUT);
+    // n_rq or more readers already counted: a counter an earlier call's timed-out merge left
+    // armed (this call's own readers add only after they have merged), so its count is stale
+    const bool stale = (seen >> 16) >= n_rq;
+    *ready_s = (seen & 0xffff) >= sp.np && !stale ? 1 : (stale ? 2 : 0);
+    if (*ready_s != 1) flag_status(p.status, PKV_STATUS_MERGE_TIMEOUT);
   }
   __syncthreads();
-  const bool ready = *ready_s;
+  const int state = *ready_s;
+  const bool ready = state == 1;
   const int r0 = 4 * rq + int(threadIdx.x >> 6);
   const int rr[1] = {r0 < p.R ? r0 : -1};
   if (ready && rr[0] >= 0)
@@ -1942,7 +1946,7 @@ __device__ __forceinline__ void merge_workgroup(const AttnParams& p, const SeqTa
       return (int64_t(slot) * G::HG + h) * p.R + r;
     });
   __syncthreads();  // every wave of this workgroup has read its parts
-  if (threadIdx.x == 0) {
+  if (threadIdx.x == 0 && state != 2) {
     const int prev = __hip_atomic_fetch_add(cnt, 1 << 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (prev == (((n_rq - 1) << 16) | sp.np)) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -3357,7 +3361,8 @@ static int decode_attn(const char* fn, bool use_scratch, const void* q, int64_t 
   const int R = s_q * (n_heads / n_kv);
   if (R > 64) return fail(PKV_EINVAL, "%s: s_q * n_heads / n_kv = %d > 64; use pkv_prefill_attn", fn, R);
   const int32_t merge = flags & (PKV_DECODE_TWO_PASS | PKV_DECODE_FUSED_MERGE);
-  if ((flags & ~(PKV_DECODE_TWO_PASS | PKV_DECODE_FUSED_MERGE | PKV_DECODE_HEADS | PKV_DECODE_GRID(0xffff))) ||
+  if ((flags & ~(PKV_DECODE_TWO_PASS | PKV_DECODE_FUSED_MERGE | PKV_DECODE_HEADS | PKV_DECODE_RESET_COUNTERS |
+                 PKV_DECODE_GRID(0xffff))) ||
       merge == (PKV_DECODE_TWO_PASS | PKV_DECODE_FUSED_MERGE))
     return fail(PKV_EINVAL, "%s: bad flags 0x%x", fn, unsigned(flags));
   if (split_tokens < 0 || split_tokens % 32)
@@ -3401,6 +3406,20 @@ static int decode_attn(const char* fn, bool use_scratch, const void* q, int64_t 
     if (!workspace || workspace_bytes < need)
       return fail(PKV_ENOSPC, "%s: workspace %zu bytes < %zu needed", fn, workspace_bytes, need);
     if (!aligned16(workspace)) return fail(PKV_EINVAL, "%s: workspace not 16-byte aligned", fn);
+    if (flags & PKV_DECODE_RESET_COUNTERS) {
+      zero_words_kernel<<<int(kCounterBytes / 4 / 256), 256, 0, s>>>(static_cast<uint32_t*>(workspace),
+                                                                       int(kCounterBytes / 4));
+      if ((rc = check_launch(fn))) return rc;
+    }
+  }
+  if (!use_scratch) {
+    // look the noalloc scratch up at the first eager decode call on the device, so that a later
+    // pkv_decode_attn_noalloc made under HIP graph capture finds it ready
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) {
+      void* unused = nullptr;
+      if (scratch_for_current_device(fn, s, &unused) != PKV_OK) clear_error();  // the noalloc call reports it
+    }
   }
 
   AttnParams p;

@@ -69,3 +69,19 @@ extern "C" int pkv_table_update(const int32_t* packet, int32_t n_len, int32_t n_
   table_update_kernel<<<(total + 255) / 256, 256, 0, static_cast<hipStream_t>(stream)>>>(p);
   return check_launch(fn);
 }
+
+namespace pkv {
+
+// The status word's bits so far, moved to *dst and cleared in one atomic exchange, so a kernel on
+// another stream that flags a bit meanwhile is never lost between a read and a clear.
+__global__ void status_take_kernel(int32_t* status, int32_t* dst) { *dst = atomicExch(status, 0); }
+
+}  // namespace pkv
+
+extern "C" int pkv_status_take(int32_t* status, int32_t* dst, void* stream) {
+  using namespace pkv;
+  clear_error();
+  if (!status || !dst) return fail(PKV_EINVAL, "pkv_status_take: null argument");
+  status_take_kernel<<<1, 1, 0, static_cast<hipStream_t>(stream)>>>(status, dst);
+  return check_launch("pkv_status_take");
+}

@@ -28,7 +28,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .attention import _require_gpu, _stream_ptr, status_tensor
+from .attention import _require_gpu, _stream_ptr, poll_status, status_tensor
 
 
 class DecodeBatch:
@@ -134,6 +134,7 @@ class DecodeBatch:
         addresses, so a graph captured on them stays valid.  cache_seqlens holds the lengths
         before the append, which are also the new tokens' rotary positions."""
         gb = len(seq_ids) if graph_batch is None else int(graph_batch)
+        poll_status(self.block_table.device)   # raises PrismKVStatusError for bits an earlier step set
         self.kv.prepare_append(list(seq_ids), n_new)
         packet, n_len, n_ent = self.plan(seq_ids, gb)
         self.apply(packet, n_len, n_ent, status)

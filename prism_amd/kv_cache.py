@@ -37,7 +37,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .attention import status_tensor
+from .attention import poll_status, status_tensor
 
 
 def shared_prefix_pages(bt_host: np.ndarray, sl_host: np.ndarray, page_size: int) -> int:
@@ -252,6 +252,8 @@ class FlashAttnKVCache:
             total = self.seq_len[sid] + n
             self._ensure_capacity(sid, total)
             self.seq_len[sid] = total
+        if torch.device(self.device).type == "cuda":
+            poll_status(self.device)
 
     def _copy_on_write(self, cow: list) -> None:
         if not cow:
@@ -299,7 +301,10 @@ class FlashAttnKVCache:
         # recorded with both tensors' version counters, so that flash_attn_with_kvcache can take
         # cascade attention for this table as long as neither has been written since
         shared = shared_prefix_pages(bt_host, sl_host, self.page_size) * self.page_size
-        bt._pkv_shared_prefix = (shared, bt._version, sl.data_ptr(), sl._version)
+        bt._pkv_shared_prefix = (shared, bt._version, sl.data_ptr(), sl._version,
+                                 int(sl_host.min()) if batch else 0)
+        if pin:
+            poll_status(self.device)   # raises PrismKVStatusError for bits an earlier call set
         return bt, sl
 
     # ------------------------------------------------------------------ page movement
@@ -400,6 +405,13 @@ class FlashAttnKVCache:
         return remap
 
 
+def _upload(rows, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+    """A small host table on the device without stalling the host: staged in pinned memory (torch's
+    caching host allocator keeps the block until the copy has run) and copied asynchronously on
+    the current stream, so copy-on-write inside a decode step does not wait for the GPU."""
+    return torch.tensor(rows, dtype=dtype).pin_memory().to(device, non_blocking=True)
+
+
 def copy_pages(src: FlashAttnKVCache, dst: FlashAttnKVCache, src_ids: list[int], dst_ids: list[int],
                fill: list[int] | None, staged: bool | None = None) -> None:
     """One pkv_copy_pages launch over every layer's K and V: dst[dst_ids[i]] <- src[src_ids[i]]
@@ -420,8 +432,7 @@ def copy_pages(src: FlashAttnKVCache, dst: FlashAttnKVCache, src_ids: list[int],
         _copy_pages_staged(src, dst, src_ids, dst_ids, fill)
         return
     dev = src.k_pool.device
-    ids = torch.tensor([list(src_ids), list(dst_ids)] + ([list(fill)] if fill is not None else []),
-                       dtype=torch.int32).to(dev, non_blocking=False)
+    ids = _upload([list(src_ids), list(dst_ids)] + ([list(fill)] if fill is not None else []), torch.int32, dev)
     lib = _lib.load()
     slot_bytes = src.num_kv_heads * src.head_dim * src.k_pool.element_size()
     page_stride = src.k_caches[0].stride(0) * src.k_pool.element_size()
@@ -442,8 +453,8 @@ def _copy_pages_staged(src: FlashAttnKVCache, dst: FlashAttnKVCache, src_ids, ds
     L2 = 2 * src.num_layers
     page_elems = src.page_size * src.num_kv_heads * src.head_dim
     staging = torch.empty((L2, n, page_elems), dtype=src.dtype, device=src.k_pool.device)
-    sbases = torch.tensor([staging[i].data_ptr() for i in range(L2)], dtype=torch.int64, device=src.k_pool.device)
-    ids = torch.tensor(list(src_ids), dtype=torch.int32, device=src.k_pool.device)
+    sbases = _upload([staging[i].data_ptr() for i in range(L2)], torch.int64, src.k_pool.device)
+    ids = _upload(list(src_ids), torch.int32, src.k_pool.device)
     esz = src.k_pool.element_size()
     lib = _lib.load()
     rc = lib.pkv_gather_pages(src.layer_bases().data_ptr(), sbases.data_ptr(), L2, ids.data_ptr(), n, 0,
@@ -452,9 +463,9 @@ def _copy_pages_staged(src: FlashAttnKVCache, dst: FlashAttnKVCache, src_ids, ds
                               torch.cuda.current_stream(src.k_pool.device).cuda_stream)
     _lib.check(rc, "pkv_gather_pages")
     remote = staging.to(dst.k_pool.device)
-    rbases = torch.tensor([remote[i].data_ptr() for i in range(L2)], dtype=torch.int64, device=dst.k_pool.device)
-    t = torch.tensor([list(range(n)), list(dst_ids)] + ([list(fill)] if fill is not None else []),
-                     dtype=torch.int32, device=dst.k_pool.device)
+    rbases = _upload([remote[i].data_ptr() for i in range(L2)], torch.int64, dst.k_pool.device)
+    t = _upload([list(range(n)), list(dst_ids)] + ([list(fill)] if fill is not None else []), torch.int32,
+                dst.k_pool.device)
     rc = lib.pkv_copy_pages(rbases.data_ptr(), dst.layer_bases().data_ptr(), L2, t[0].data_ptr(), t[1].data_ptr(),
                             t[2].data_ptr() if fill is not None else 0, n, page_elems * esz,
                             dst.k_caches[0].stride(0) * esz, src.num_kv_heads * src.head_dim * esz, src.page_size,

@@ -173,11 +173,12 @@ def config3(device="cuda", seed=0, layers=None, max_pages=None, batch=32, churn=
 
 
 def ragged_decode(shape: str, device="cuda", seed=0, layers=None, max_pages=None, batch=32, churn=0.4,
-                  budget_gb=30.0) -> PagedWorkload:
+                  budget_gb=30.0, force: dict[int, int] | None = None, name: str | None = None) -> PagedWorkload:
     """config3's ragged decode batch (lognormal lengths, churned pool, LIFO allocation) at another
     model shape: the Qwen2.5-14B (8 KV heads) and 0.5B (2 KV heads, head_dim 64) decode steps, and
     the 7B step on one GPU of a 4-way tensor-parallel group (1 KV head).  The pool is the model's
-    30 GB budget, capped at 4096 pages."""
+    30 GB budget, capped at 4096 pages.  force {index: context} replaces drawn lengths (the long
+    end of config 3's [16, 32768] range)."""
     s = SHAPES[shape]
     L = layers or s["layers"]
     rng = np.random.default_rng(seed)
@@ -186,14 +187,49 @@ def ragged_decode(shape: str, device="cuda", seed=0, layers=None, max_pages=None
     g = _gen(device, seed)
     _fill_pool(kv, g)
     ctx = lognormal_ctx(rng, batch)
+    for i, c in (force or {}).items():
+        ctx[i] = c
     freed = rng.permutation(mp)[: int(round(churn * mp))]
     need = int(np.ceil((ctx + 1) / PAGE).sum())
     if need > len(freed):
         raise RuntimeError(f"ragged_decode {shape} seed {seed}: {need} pages needed > {len(freed)} free")
     kv.free_pages = [int(p) for p in freed]
     _alloc(kv, range(batch), ctx, 1)
-    return _finish(f"decode-{shape}", kv, list(range(batch)), ctx, 1, s["n_heads"], g, device,
+    return _finish(name or f"decode-{shape}", kv, list(range(batch)), ctx, 1, s["n_heads"], g, device,
                    {"shape": shape, "pool_pages": mp})
+
+
+# config 3's long end: a sequence at the 32768-token clip (32767 keys before the append) beside a
+# 12000-token one, in the seed's ragged batch; and one sequence alone at the clip (the B = 1 graph)
+LONG_FORCE = {0: 32767, 1: 12000}
+
+
+def long_decode(device="cuda", seed=0, layers=None, shape: str = "7B", batch: int = 32) -> PagedWorkload:
+    """Decode past the executor's 32-page graph limit (engine/executor.py:343, :385-386): config 3's
+    ragged 7B batch with sequence 0 at 32767 cached keys and sequence 1 at 12000 (batch > 1), or a
+    single sequence at 32767 keys (batch = 1)."""
+    force = {0: LONG_FORCE[0]} if batch == 1 else dict(LONG_FORCE)
+    name = f"long-decode-{shape}-b{batch}"
+    return ragged_decode(shape, device, seed=seed, layers=layers, batch=batch, force=force, name=name)
+
+
+def prompt_prefill(device="cuda", seed=0, layers=None, shape: str = "7B", prompt: int = 4096,
+                   batch: int = 1) -> PagedWorkload:
+    """Whole-prompt prefill (engine/executor.py:97-120): `batch` sequences with no cached prefix, each
+    appending and attending a `prompt`-token chunk (causal), on the model's 30 GB pool with pages
+    scattered by a seeded permutation of the free list."""
+    s = SHAPES[shape]
+    L = layers or s["layers"]
+    rng = np.random.default_rng(seed)
+    mp = pages_for_budget(30.0, s["layers"], s["n_kv"], s["head_dim"])
+    kv = FlashAttnKVCache(L, s["n_kv"], s["head_dim"], mp, PAGE, device, torch.bfloat16)
+    g = _gen(device, seed)
+    _fill_pool(kv, g)
+    kv.free_pages = [int(p) for p in rng.permutation(mp)]
+    ctx = np.zeros(batch, dtype=np.int64)
+    _alloc(kv, range(batch), ctx, prompt)
+    return _finish(f"prefill-{shape}-{prompt}", kv, list(range(batch)), ctx, prompt, s["n_heads"], g, device,
+                   {"shape": shape})
 
 
 def config4(device="cuda", seed=0, layers=None, max_pages=None, batch=8, chunk=512, max_prefix=4096) -> PagedWorkload:

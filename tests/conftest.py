@@ -39,9 +39,9 @@ def _gpu_status_clean(request):
 
     if not torch.cuda.is_available():
         return
-    from prism_amd.attention import _status
+    from prism_amd.attention import _status, read_status
 
-    for t in _status.values():
-        v = int(t.item())
-        t.zero_()
+    for idx in list(_status):
+        # the device word and whatever a poll_status has moved to the host meanwhile
+        v = read_status(torch.device("cuda", idx), clear=True)
         assert v == 0, f"kernel status flags set: {v}"

@@ -34,7 +34,7 @@ def test_header_constants_match_binding(lib):
     defines = dict(re.findall(r"^#define (PKV_\w+) \(?(-?\d+)\)?", HEADER, re.M))
     for name in ["PKV_OK", "PKV_EINVAL", "PKV_EHIP", "PKV_ENOSPC", "PKV_STATUS_BAD_PAGE", "PKV_STATUS_BAD_POSITION",
                  "PKV_STATUS_SHARED_PREFIX", "PKV_STATUS_PARTIAL_RANGE", "PKV_STATUS_MERGE_TIMEOUT", "PKV_DECODE_TWO_PASS",
-                 "PKV_DECODE_FUSED_MERGE", "PKV_DECODE_HEADS"]:
+                 "PKV_DECODE_FUSED_MERGE", "PKV_DECODE_HEADS", "PKV_DECODE_RESET_COUNTERS"]:
         assert int(defines[name]) == getattr(_lib, name), name
     assert int(defines["PKV_ABI_VERSION"]) == _lib.ABI_VERSION == lib.pkv_abi_version()
     assert lib.pkv_last_error() == b""

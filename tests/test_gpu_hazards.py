@@ -106,3 +106,99 @@ def test_capture_on_a_fresh_stream_after_eager_warmup(gpu, s_q):
                                                cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"],
                                                causal=True)
     assert_attn_close(out, ref, f"captured s_q={s_q}")
+
+
+def test_status_bits_reach_the_host_at_build_block_table(gpu):
+    # the short-capacity write of the test above, then the host points Prism passes every step:
+    # the first build_block_table starts an asynchronous read of the status word, a later one
+    # raises PrismKVStatusError with the bit (nothing on the host waited for the GPU)
+    kv = prism_amd.FlashAttnKVCache(1, 4, 128, 8, 256, str(gpu))
+    kv.new_sequence(0)
+    kv._ensure_capacity(0, 300)
+    kv.seq_len[0] = 299
+    kv.new_sequence(1)
+    kv.seq_len[1] = 256
+    bt, sl = kv.build_block_table([0, 1])
+    g = torch.Generator(device=gpu).manual_seed(5)
+    q = torch.randn(2, 1, 28, 128, generator=g, device=gpu).to(torch.bfloat16)
+    k = torch.randn(2, 1, 4, 128, generator=g, device=gpu).to(torch.bfloat16)
+    prism_amd.flash_attn_with_kvcache(q, kv.k_caches[0], kv.v_caches[0], k=k, v=k.clone(), cache_seqlens=sl,
+                                      block_table=bt, causal=True)
+    kv.build_block_table([0, 1])          # starts the read; nothing has landed yet
+    torch.cuda.synchronize()
+    with pytest.raises(prism_amd.PrismKVStatusError) as e:
+        kv.build_block_table([0, 1])
+    assert e.value.bits & prism_amd._lib.PKV_STATUS_BAD_PAGE and "BAD_PAGE" in str(e.value)
+    # reported once: the word and the host copies are clear again
+    torch.cuda.synchronize()
+    kv.update_seqlens([0], 1)
+    assert prism_amd.read_status(gpu) == 0
+
+
+def test_stale_merge_counters_are_flagged_then_cleared(gpu):
+    # a merge that timed out leaves its arrival counter armed; the next call's merge workgroups
+    # must flag PKV_STATUS_MERGE_TIMEOUT instead of merging stale partials, and reading the bit
+    # clears the workspace's counters so that the call after it is right again.  The leftover
+    # state is planted from the host (every counter word set), so every kernel exits normally.
+    from prism_amd import attention as attn
+    cpu, dev = make_paged_case(gpu, batch=3, ctx=[3000, 17, 4100], page_size=256, n_kv=4, n_heads=28,
+                               head_dim=128, s_q=1, seed=21)
+    kw = dict(cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"], causal=True, two_pass=False,
+              grid=8)
+    good = prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], **kw)
+    torch.cuda.synchronize()
+    assert prism_amd.read_status(gpu) == 0
+    ref, _, _ = pa.flash_attn_with_kvcache_ref(cpu["q"], cpu["k_cache"], cpu["v_cache"],
+                                               cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"],
+                                               causal=True)
+    assert_attn_close(good, ref, "in-launch merge, 8 workgroups")
+    ws = attn._workspaces[(gpu.index or 0, torch.cuda.current_stream(gpu).cuda_stream)]
+    ws[:65536].view(torch.int32).fill_(0x7FFF7FFF)
+    out = torch.full_like(good, float("nan"))
+    prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], out=out, **kw)
+    torch.cuda.synchronize()
+    assert prism_amd.read_status(gpu) & prism_amd._lib.PKV_STATUS_MERGE_TIMEOUT
+    assert not torch.equal(out, good)      # the split sequences' rows were left unwritten
+    torch.cuda.synchronize()
+    assert int(ws[:65536].view(torch.int32).abs().sum()) == 0   # read_status cleared the counters
+    again = prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(again, good)
+    assert prism_amd.read_status(gpu) == 0
+    # the noalloc scratch is cleared by the flag its next call then carries
+    attn._reset_counters.add(gpu.index or 0)
+    na = prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], noalloc=True, **kw)
+    torch.cuda.synchronize()
+    assert not attn._reset_counters and torch.equal(na, good)
+
+
+@pytest.mark.parametrize("prefix,s_q", [(2560, 5), (2048, 2)])
+def test_no_append_causal_verify_cuts_the_automatic_cascade_prefix(gpu, prefix, s_q):
+    # 8 branches of one prompt on full shared pages, called the way flash_attn allows without an
+    # append: causal query row 0 sees keys t <= L - s_q only, so the automatic cascade may read
+    # only the whole pages below that as a shared prefix (2560 keys, s_q 5: 2304, still a
+    # cascade; 2048, s_q 2: 1792, below the automatic threshold: the ordinary path).  A prefix
+    # that row 0 cannot see whole would flag PKV_STATUS_SHARED_PREFIX and give row 0 a key it
+    # must not see.
+    kv = prism_amd.FlashAttnKVCache(1, 4, 128, 24, 256, str(gpu))
+    g = torch.Generator(device=gpu).manual_seed(prefix + s_q)
+    kv.k_pool.normal_(generator=g)
+    kv.v_pool.normal_(generator=g)
+    kv.new_sequence(100)
+    kv._ensure_capacity(100, prefix)
+    kv.seq_len[100] = prefix
+    ids = list(range(8))
+    for sid in ids:
+        kv.fork_sequence(100, sid)
+    bt, sl = kv.build_block_table(ids)
+    want = (prefix - s_q + 1) // 256 * 256
+    assert prism_amd.shared_prefix_of(bt, sl, s_q=s_q, causal=True, appends=False, page_size=256) == want
+    q = torch.randn(8, s_q, 28, 128, generator=g, device=gpu).to(torch.bfloat16)
+    kc, vc = kv.k_caches[0].cpu(), kv.v_caches[0].cpu()
+    out = prism_amd.flash_attn_with_kvcache(q, kv.k_caches[0], kv.v_caches[0], cache_seqlens=sl, block_table=bt,
+                                            causal=True)
+    torch.cuda.synchronize()
+    assert prism_amd.read_status(gpu) == 0
+    ref, _, _ = pa.flash_attn_with_kvcache_ref(q.cpu(), kc, vc, cache_seqlens=sl.cpu(),
+                                               block_table=bt.cpu().clamp(min=0), causal=True)
+    assert_attn_close(out, ref, f"no-append causal verify, prefix {prefix}, s_q {s_q}")

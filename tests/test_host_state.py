@@ -262,6 +262,14 @@ def test_build_block_table_records_the_shared_prefix(copies):
         kv.fork_sequence(0, sid)
     bt, sl = kv.build_block_table([0, 1, 2, 3])
     assert shared_prefix_of(bt, sl) == 32
+    # without an append, causal query row 0 sees keys t <= 40 - s_q: the prefix is cut to the
+    # whole pages below that (39 keys -> 2 pages, 31 -> 1, 11 -> none); an append or a
+    # non-causal call keeps it
+    assert shared_prefix_of(bt, sl, s_q=2, causal=True, appends=False, page_size=16) == 32
+    assert shared_prefix_of(bt, sl, s_q=10, causal=True, appends=False, page_size=16) == 16
+    assert shared_prefix_of(bt, sl, s_q=30, causal=True, appends=False, page_size=16) == 0
+    assert shared_prefix_of(bt, sl, s_q=30, causal=False, appends=False, page_size=16) == 32
+    assert shared_prefix_of(bt, sl, s_q=30, causal=True, appends=True, page_size=16) == 32
     kv.prepare_append([0, 1, 2, 3], 5)
     bt, sl = kv.build_block_table([0, 1, 2, 3])
     assert len(set(bt[:, 2].tolist())) == 4 and shared_prefix_of(bt, sl) == 32

@@ -118,6 +118,25 @@ def test_attention_matches_sdpa_full_square_causal(nh, n_kv, hd):
     np.testing.assert_allclose(out, ref.transpose(1, 2).numpy(), rtol=1e-10, atol=1e-12)
 
 
+def test_attention_row_sample_matches_sdpa_rows():
+    # a sample of query rows (what the long-prefill parity tests check) against torch's SDPA on the
+    # full square causal case: each sampled row keeps its own causal limit
+    rng = np.random.default_rng(41)
+    B, L, P, nh, n_kv, hd = 2, 45, 8, 6, 2, 32
+    K = _rand_bits((B, L, n_kv, hd), rng)
+    V = _rand_bits((B, L, n_kv, hd), rng)
+    pk, pv, bt = _paged_from_dense(K, V, P, rng)
+    q = _rand_bits((B, L, nh, hd), rng)
+    rows = np.array([0, 1, 7, 8, 30, 44])
+    out = pa.attention_fp64(q, pk, pv, bt, np.array([L, L]), causal=True, rows=rows)
+    assert out.shape == (B, len(rows), nh, hd)
+    qt = torch.from_numpy(pa.bits_to_f64(q)).transpose(1, 2)
+    kt = torch.from_numpy(pa.bits_to_f64(K)).transpose(1, 2)
+    vt = torch.from_numpy(pa.bits_to_f64(V)).transpose(1, 2)
+    ref = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, is_causal=True, enable_gqa=True)
+    np.testing.assert_allclose(out, ref.transpose(1, 2).numpy()[:, rows], rtol=1e-10, atol=1e-12)
+
+
 def test_attention_matches_sdpa_non_causal_default_scale():
     rng = np.random.default_rng(7)
     B, L, P, nh, n_kv, hd = 3, 50, 16, 8, 2, 64
