@@ -130,9 +130,8 @@ size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, i
  * page_size must hold a whole tile); the sequences that straddle shares are merged by a second
  * launch (PKV_DECODE_TWO_PASS) or, for decode's <= 16 query rows per KV head, inside the launch
  * by merge workgroups that wait for a sequence's shares (PKV_DECODE_FUSED_MERGE).  With neither
- * flag the library merges inside the launch when batch * ceil(max_blocks * page_size / tile
- * tokens) * (n_kv / heads per tile) is at most 6 tiles per workgroup (small, launch-bound calls),
- * else in a second launch.
+ * flag the library merges inside the launch when those merge workgroups, batch * n_kv *
+ * ceil(R / 4), are no more than the decode workgroups (one per CU), else in a second launch.
  * Otherwise a per-(sequence, KV head, split) kernel reduces split_tokens keys (a multiple of 32;
  * 0 = 512) per workgroup and merges the splits inside the launch (PKV_DECODE_TWO_PASS: in a
  * second launch).  Results agree up to rounding (fp32 order, fp16 split-K partials).

@@ -371,9 +371,11 @@ def flash_attn_with_kvcache(
     fixes the number of KV splits per sequence; ``split_tokens`` > 0 (a multiple of 32) fixes
     the split length directly (both select the per-head kernel); ``two_pass`` True merges the
     split-K partials in a second launch, False inside the attention launch (by the last split to
-    finish, or by merge workgroups of the balanced kernel), None lets the library choose (a second launch for the
-    balanced kernel, in-launch for the per-head kernel).  ``kernel="heads"`` forces the per-head kernel where the balanced one would
-    run; ``grid`` > 0 runs the balanced kernel on that many workgroups instead of one per CU.
+    finish, or by merge workgroups of the balanced kernel), None lets the library choose (the
+    per-head kernel merges in the launch; the balanced kernel does when its merge workgroups,
+    batch * n_kv * ceil(s_q * n_heads / n_kv / 4), are no more than its CUs, and decode rows
+    only).  ``kernel="heads"`` forces the per-head kernel where the balanced one would run;
+    ``grid`` > 0 runs the balanced kernel on that many workgroups instead of one per CU.
 
     ``shared_prefix_tokens`` > 0 (a multiple of the page size) declares that every sequence of
     the batch lists the same pages for its first shared_prefix_tokens keys and holds at least

@@ -3126,9 +3126,6 @@ static void launch_lean(const AttnParams& p, int head_dim, int R, int batch, int
     default: break;
   }
 }
-// Merge mode of a balanced call without a merge flag: in the launch when the block table's
-// capacity is at most this many tiles per workgroup.
-constexpr int kFusedMaxTilesPerWg = 6;
 
 static int lean_heads_per_group(int head_dim, int n_kv) {
   switch (lean_geom(head_dim, n_kv)) {
@@ -3431,27 +3428,23 @@ static int decode_attn(const char* fn, bool use_scratch, const void* q, int64_t 
   p.rot_sin = static_cast<const uint16_t*>(rot_sin);
   p.n_pos = n_pos;
   if (lean) {
-    // balanced row-streaming kernel; partials merged by a second launch, or inside the launch
-    // with PKV_DECODE_FUSED_MERGE (slower on the 7B decode step: the merge of a long sequence's
-    // ~27 parts by its last range costs more than the second launch)
     p.ws_cnt = static_cast<int32_t*>(workspace);
     p.ws_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
     p.ws_ml = lean_lse_base(p.ws_o, size_t(2) * grid, R);
-    // in-launch merge only for decode rows (R <= 16): verify's row count would need too many
-    // merge workgroups, so it always merges in a second launch.  Without a merge flag the call
-    // merges in the launch when the block table bounds it to kFusedMaxTilesPerWg tiles per
-    // workgroup: such a call is bound by fixed costs, and the in-launch merge saves the second
-    // launch's (7B at B = 8, 0.5B and 7B TP-4 shards of a 32-sequence ragged batch: 17.3-17.5 /
-    // 15.6 / 18.4 us per call against 17.5-17.6 / 16.1-16.3 / 19.6 two-pass), while the longer
-    // streams of bigger calls finish sooner with the second launch (7B at B = 32: 29.5 against
-    // 28.8-29.3, 14B: 47.2-48.1 against 46.3).
+    // balanced row-streaming kernel; partials merged by a second launch, or inside the launch by
+    // merge workgroups appended to the grid (decode rows only: verify's row count would need too
+    // many merge workgroups, so it always merges in a second launch).  Without a merge flag the
+    // call merges in the launch when its merge workgroups (one per sequence, KV head and 4 query
+    // rows) are at most one per CU, one round of the CUs as the decode workgroups leave them: each
+    // then starts as soon as a decode workgroup has left its CU and merges without the second
+    // launch's dispatch.  Measured per call, in the launch against
+    // a second launch (interleaved on one box): 7B at B = 32 28.4-28.9 against 28.9 us, with a
+    // 32767-key and a 12000-key sequence in that batch 41.8-42.1 against 45.0-45.2, one 32767-key
+    // sequence 25.9 against 32.0, B = 8 16.2 against 17.0, the 0.5B and 7B TP-4 shapes of the
+    // B = 32 batch 15.6-15.7 against 16.0 and 18.1 against 19.2.  The 14B shape's 512 merge
+    // workgroups take two rounds of the CUs: 44.7-44.9 us with the second launch, 46.9-47.7 in it.
     bool fused = merge == PKV_DECODE_FUSED_MERGE;
-    if (merge == 0) {
-      const int hg = lean_heads_per_group(head_dim, n_kv);
-      const int64_t tok = int64_t(rows::TILE) * (4 / hg) * (128 / head_dim);  // tokens per tile
-      const int64_t tiles = int64_t(n_kv / hg) * batch * ((int64_t(max_blocks) * page_size + tok - 1) / tok);
-      fused = tiles <= int64_t(kFusedMaxTilesPerWg) * grid;
-    }
+    if (merge == 0) fused = int64_t(batch) * n_kv * ((R + 3) / 4) <= grid;
     p.two_pass = fused && R <= 16 ? 0 : 1;
     // the counters 128 bytes apart where the counter region has room
     p.cnt_stride = 1;
@@ -3459,6 +3452,8 @@ static int decode_attn(const char* fn, bool use_scratch, const void* q, int64_t 
     p.lean_grid = grid;
     p.n_groups = n_kv / lean_heads_per_group(head_dim, n_kv);
     p.tok_elems = n_kv * head_dim;
+    // every balanced launch writes split-K partials and counters: never launch one without them
+    if (!p.ws_cnt || !p.ws_o || !p.ws_ml) return fail(PKV_EINVAL, "%s: balanced launch without a workspace", fn);
     launch_lean(p, head_dim, R, batch, grid, s);
     return check_launch(fn);
   }
@@ -3626,6 +3621,7 @@ extern "C" int pkv_cascade_attn(const void* q, int64_t q_sb, int64_t q_ss, int64
   p.tok_elems = n_kv * head_dim;
   p.k0 = shared_tokens;
   p.cascade_splits = S;
+  if (!p.ws_cnt || !p.ws_o || !p.ws_ml) return fail(PKV_EINVAL, "%s: cascade launch without a workspace", fn);
   hipStream_t s = static_cast<hipStream_t>(stream);
   constexpr int NT = PKV_PREFILL_LDS_NT, W = PKV_PREFILL_LDS_W;
   const dim3 pgrid((batch * R + 16 * NT * W - 1) / (16 * NT * W), rows::NKV, S);
