@@ -758,7 +758,8 @@ def main() -> int:
                 "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
                 "kernel": "one pkv_decode_attn call = decode_lean_kernel (append + balanced paged attention, "
-                          "split-K partials) + combine_lean_kernel (merge); " + per_call,
+                          "split-K partials merged by workgroups appended to the launch; a second "
+                          "combine_lean_kernel launch when those exceed one per CU); " + per_call,
                 "bytes_per_call": bytes_layer, "avg_call_us": round(call_us, 3),
             },
         }
