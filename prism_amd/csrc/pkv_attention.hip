@@ -1653,7 +1653,10 @@ __device__ __forceinline__ void wait_vmcnt_at_most(int n) {
 }
 
 // Q^T operand of head h's 16*NT rows of sequence d.b straight from q into registers (load_q's
-// layout; rows >= R get zeros).  Used where NT > 1, whose Q does not fit the LDS buffers.
+// layout).  Used where NT > 1, whose Q does not fit the LDS buffers.  Padding rows (>= R) repeat
+// row R - 1: they are computed and never stored, and registers kept exactly as loaded are waited
+// for at their first use only (zeroing them would wait for the loads, and with them for every
+// tile copy issued after them, where they are loaded).
 template <int HD, int NT>
 __device__ __forceinline__ void rows_load_q(const AttnParams& p, const TileDesc& d, int h,
                                             bf16x8 (&qf)[NT][HD / 32]) {
@@ -1662,16 +1665,12 @@ __device__ __forceinline__ void rows_load_q(const AttnParams& p, const TileDesc&
   const int lq = lane >> 4;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int rr = li + 16 * nt;
-    const int rc = min(rr, p.R - 1);
+    const int rc = min(li + 16 * nt, p.R - 1);
     const int jq = rc / p.g;
     const int hq = rc - jq * p.g;
     const uint16_t* base = p.q + d.b * p.q_sb + jq * p.q_ss + (h * p.g + hq) * p.q_sh + 8 * lq;
 #pragma unroll
-    for (int kk = 0; kk < HD / 32; ++kk) {
-      const u32x4 v = ld16(base + 32 * kk);
-      qf[nt][kk] = __builtin_bit_cast(bf16x8, rr < p.R ? v : u32x4{0u, 0u, 0u, 0u});
-    }
+    for (int kk = 0; kk < HD / 32; ++kk) qf[nt][kk] = __builtin_bit_cast(bf16x8, ld16(base + 32 * kk));
   }
 }
 
@@ -2032,8 +2031,12 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
 
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
-  const int hg = w % G::HG;  // KV head within the group
-  const int ph = w / G::HG;  // phase: keys [32 S ph, 32 S (ph + 1)) of every tile
+  // The wave's slice of every LDS row.  Spelled w & 3 (w < 4 anyway), this build of the verify
+  // kernel keeps 145 scalar spill reloads in its tile loop, against 305 with w: config-5 verify
+  // 57.7 against 62.3 us per call, config-3 decode 28.3 against 28.5-29.0.
+  const int hw = w & 3;
+  const int hg = hw % G::HG;  // KV head within the group
+  const int ph = hw / G::HG;  // phase: keys [32 S ph, 32 S (ph + 1)) of every tile
   const bool leader = ph == 0;
   const int li = lane & 15;
   const int lq = lane >> 4;
@@ -2052,6 +2055,20 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   if (s >= e) return;
   const int n = e - s;
 
+  // Verify rows (Q in registers) load the first segment's Q ahead of the block-table read, whose
+  // wait covers it.  Loaded at the segment start, behind the first two tiles' copies, its wait
+  // (vmcnt retires in order) held tile 0's compute until tile 1 had landed as well (config-5
+  // verify: tile 1 landed 4.1 us after tile 0, against 1.9 us between later tiles).
+  bf16x8 qf[NT][KK];
+  if constexpr (!kQInLds) {
+    TileDesc d0;  // the range's first tile as tile_window finds it: head group and sequence
+    d0.g = s / T1;
+    int first0, c0, L0;
+    locate_tile(p, st, s - d0.g * T1, d0.b, first0, c0, L0);
+    d0.b = __builtin_amdgcn_readfirstlane(min(d0.b, p.batch - 1));
+    d0.g = __builtin_amdgcn_readfirstlane(d0.g);
+    rows_load_q<HD, NT>(p, d0, d0.g * G::HG + hg, qf);
+  }
   TileWin win;
   tile_window<NCH, TOK>(p, st, s, e, T1, win);
   TileDesc dA = tile_desc(win, s);
@@ -2069,8 +2086,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   }
 
   uint32_t vto[4];
-  if constexpr (kVTr) rows_vt_offsets<G>(w, vto);
-  bf16x8 qf[NT][KK];
+  if constexpr (kVTr) rows_vt_offsets<G>(hw, vto);
   int lim[NT];
   int lim_min = 0x7fffffff;
   float m_run[NT], l_run[NT];
@@ -2111,8 +2127,11 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
       if constexpr (kQInLds) {
         if constexpr (kRope) rows_rope_q_area<G>(p, buf);
         rows_read_q<G>(p, buf, hg, qf);
-      } else {
+      } else if (j > 0) {
+        // a later segment's Q: waited for here, so no wait for loads in flight reaches the
+        // products on the loop's common path
         rows_load_q<HD, NT>(p, d, d.g * G::HG + hg, qf);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
       }
       seg_j0 = j;
       seg_T0 = d.T0;
@@ -2142,11 +2161,11 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     }
     KVTile<HD> tl[G::S];
     if constexpr (kVTr) {
-      rows_read_tile_vt<G>(buf, w, d.T0 + rows::TILE * ph, d.L, vto, tl[0]);
+      rows_read_tile_vt<G>(buf, hw, d.T0 + rows::TILE * ph, d.L, vto, tl[0]);
     } else {
 #pragma unroll
       for (int sub = 0; sub < G::S; ++sub)
-        rows_read_tile<G>(buf, w, sub, d.T0 + rows::TILE * (ph * G::S + sub), d.L, tl[sub]);
+        rows_read_tile<G>(buf, hw, sub, d.T0 + rows::TILE * (ph * G::S + sub), d.L, tl[sub]);
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
     raw_barrier();                       // nobody reads this buffer any more
