@@ -781,7 +781,7 @@ def main() -> int:
             "roofline": {
                 "bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
-                "kernel": "one pkv_prefill_attn call = append_kernel + prefill_lds_kernel<2,4,2,1> (LDS-staged KV tiles, 128 query rows per workgroup); " + per_call,
+                "kernel": "one pkv_prefill_attn call = append_kernel + prefill_lds_kernel<2,4,4,1> (LDS-staged KV tiles in 4 stages, 128 query rows per workgroup); " + per_call,
                 "flops_per_call": flops_layer, "bytes_per_call": bytes_layer, "avg_call_us": round(call_us, 3),
                 "hbm_gbs": round(gbs, 1),
             },

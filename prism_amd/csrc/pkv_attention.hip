@@ -2516,7 +2516,12 @@ __device__ __forceinline__ void pf_qk(const u32x4 (&kr)[2][4], const bf16x8 (&qf
 // exponentials, one MFMA between every few vector instructions: a wave issues in order and its
 // next MFMA waits for the matrix pipe, so products placed back to back would hold the softmax
 // behind them, while interleaved the two pipes work at once.
-template <int NT, bool NEXT, typename LT, typename VOps>
+// PRIO: the PV products issue at raised wave priority.  With two waves per SIMD (prefill), the
+// wave holding its PV products then wins the issue slots over the other wave's exponentials
+// whenever the matrix pipe can take a product, so the two waves drift into opposite phases
+// instead of queueing for the same pipe (prefill-4096 142.7 -> 132.8 us; verify, at one wave per
+// SIMD, 57.7 -> 58.0, so it stays off there).
+template <int NT, bool NEXT, bool PRIO = false, typename LT, typename VOps>
 __device__ __forceinline__ void pf_softmax_pv(const AttnParams& p, f32x4 (&s)[NT][2], const u32x4 (&kn)[2][4],
                                               f32x4 (&sn)[NT][2], VOps&& v_ops, int T0, const bf16x8 (&qf)[NT][4],
                                               const int (&lim)[NT], int lim_min, float (&m_run)[NT],
@@ -2600,11 +2605,13 @@ __device__ __forceinline__ void pf_softmax_pv(const AttnParams& p, f32x4 (&s)[NT
   }
   bf16x8 vt[DPL];
   v_ops(vt);
+  if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int n = 0; n < DPL; ++n)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
       acc[nt][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[n], pb[nt], acc[nt][n], 0, 0, 0);
+  if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
 }
 
 template <int NT, typename LT, typename VIssue, typename VOps>
@@ -2879,7 +2886,7 @@ __global__ __launch_bounds__(64 * W) void prefill_lds_kernel(const AttnParams p)
       u32x4 kn[2][4];
       f32x4 sn[NT][2];
       if constexpr (NEXT) read_k(t + 1, kn);
-      pf_softmax_pv<NT, NEXT>(p, s, kn, sn, v_ops, T0, qf, lim, lim_min, m_run, l_run, acc);
+      pf_softmax_pv<NT, NEXT, true>(p, s, kn, sn, v_ops, T0, qf, lim, lim_min, m_run, l_run, acc);
       if constexpr (NEXT) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
