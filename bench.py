@@ -59,6 +59,7 @@ def parse():
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = library choice)")
     ap.add_argument("--grid", type=int, default=0, help="workgroups of the balanced kernel (0 = one per CU)")
     ap.add_argument("--layers", type=int, default=0, help="layers (0 = the model's)")
+    ap.add_argument("--batch", type=int, default=0, help="config2's batch at context 2048 (0 = its own 8)")
     ap.add_argument("--merge", choices=["auto", "two-pass", "fused"], default="auto",
                     help="split-K merge of the per-head kernel: library choice, second launch, in-launch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -683,6 +684,8 @@ def main() -> int:
                                   batch=1 if args.workload.endswith("-b1") else 32)
     elif args.workload == "prefill-4096":
         w = workloads.prompt_prefill(dev, seed=args.seed, layers=args.layers or None, prompt=4096)
+    elif args.workload == "config2" and args.batch:
+        w = workloads.config2(dev, seed=args.seed, layers=args.layers or None, batch=args.batch)
     else:
         w = getattr(workloads, args.workload)(dev, seed=args.seed, layers=args.layers or None)
     L = w.layers
@@ -748,9 +751,9 @@ def main() -> int:
             cfg["workload"] = (f"{args.workload}: config3's ragged batch (b={w.batch}, ctx lognormal(1500, 1), 40% "
                                f"churn) at the Qwen2.5-{shape} shape, {L} layers, {kv.max_pages}-page pool")
         else:
-            metric = "paged decode attn HBM GB/s (% of peak) + us/step, Qwen2.5-7B shape b=8 ctx 2048"
-            cfg["workload"] = ("config2: Qwen2.5-7B paged decode (append + attention), 28 layers, b=8, ctx 2048, "
-                               "2043-page 30 GB pool")
+            metric = f"paged decode attn HBM GB/s (% of peak) + us/step, Qwen2.5-7B shape b={w.batch} ctx 2048"
+            cfg["workload"] = (f"config2: Qwen2.5-7B paged decode (append + attention), 28 layers, b={w.batch}, "
+                               "ctx 2048, 2043-page 30 GB pool")
         result = {
             "metric": metric, "value": round(bytes_layer * L / (step_ms * 1e-3) / 1e9, 2), "unit": "GB/s",
             **common, "pct_of_peak_hbm": round(100 * gbs / HBM_PEAK_GBS, 2), "config": cfg,
