@@ -117,6 +117,50 @@ def test_noalloc_rejects_a_call_beyond_its_scratch(gpu):
     assert int(status.item()) == 0
 
 
+def test_noalloc_never_takes_the_cascade(gpu):
+    # a forked-branch verify batch whose table would send the default call to cascade attention
+    # (which needs a workspace of the module's): with noalloc it runs the allocation-free decode
+    # entry point, allocates nothing and matches the oracle
+    import numpy as np
+
+    import prism_amd
+    from prism_amd import shared_prefix_of
+
+    P, n_kv, hd, nh, s_q = 256, 4, 128, 28, 5
+    kv = prism_amd.FlashAttnKVCache(1, n_kv, hd, 64, P, str(gpu))
+    g = torch.Generator().manual_seed(11)
+    kv.k_pool.copy_(torch.randn(kv.k_pool.shape, generator=g).to(torch.bfloat16))
+    kv.v_pool.copy_(torch.randn(kv.v_pool.shape, generator=g).to(torch.bfloat16))
+    kv.new_sequence(0)
+    kv._ensure_capacity(0, 2400)
+    kv.seq_len[0] = 2400
+    ids = list(range(8))
+    for sid in ids[1:]:
+        kv.fork_sequence(0, sid)
+    for sid in ids:
+        grow = (sid * 53) % 300
+        kv.prepare_append([sid], grow)
+        kv.update_seqlens([sid], grow)
+    bt, sl = kv.build_block_table(ids)
+    assert shared_prefix_of(bt, sl, s_q=s_q, appends=False) >= prism_amd.attention.AUTO_CASCADE_MIN_TOKENS
+    q = torch.randn(len(ids), s_q, nh, hd, generator=g).to(torch.bfloat16).to(gpu)
+    out = torch.full_like(q, float("nan"))
+    kw = dict(cache_seqlens=sl, block_table=bt, causal=True, noalloc=True, out=out)
+    print(f"noalloc forked branches B={len(ids)} s_q={s_q}", flush=True)
+    prism_amd.flash_attn_with_kvcache(q, kv.k_caches[0], kv.v_caches[0], **kw)  # first use: status words
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated(gpu)
+    out.fill_(float("nan"))
+    prism_amd.flash_attn_with_kvcache(q, kv.k_caches[0], kv.v_caches[0], **kw)
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated(gpu) == before, "the noalloc call allocated device memory"
+    ref, _, _ = pa.flash_attn_with_kvcache_ref(q.cpu(), kv.k_caches[0].cpu(), kv.v_caches[0].cpu(),
+                                               cache_seqlens=sl.cpu(), block_table=bt.cpu(), causal=True)
+    assert np.isfinite(out.float().cpu().numpy()).all()
+    assert_attn_close(out, ref, "noalloc forked branches")
+    assert prism_amd.read_status(gpu) == 0
+
+
 def test_noalloc_inside_a_captured_graph(gpu):
     # the drop-in's noalloc path captured on a fresh stream (nothing allocated during capture);
     # replays equal the eager call, with eager calls on the shared scratch between the replays
