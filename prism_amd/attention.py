@@ -74,6 +74,7 @@ class PrismKVStatusError(RuntimeError):
         super().__init__(f"prism_amd kernel status on cuda:{device}: {'|'.join(names)} ({bits}) "
                          "(see PKV_STATUS_* in include/prism_kv.h)")
         self.bits = bits
+        self.device = device
 
 
 class _StatusCopies:

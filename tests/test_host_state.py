@@ -295,3 +295,14 @@ def test_build_block_table_records_the_shared_prefix(copies):
     assert shared_prefix_pages(t[:1], np.array([64]), 16) == 0
     assert shared_prefix_pages(np.full((2, 3), -1, dtype=np.int32), np.array([0, 0]), 16) == 0
     _check_invariants(kv)
+
+
+def test_status_error_names_every_bit():
+    # the exception a status poll raises carries the bits and the device, and names each flag
+    from prism_amd import PrismKVStatusError
+    from prism_amd import _lib
+    bits = _lib.PKV_STATUS_BAD_PAGE | _lib.PKV_STATUS_MERGE_TIMEOUT
+    e = PrismKVStatusError(bits, 3)
+    assert e.bits == bits and e.device == 3 and isinstance(e, RuntimeError)
+    assert "BAD_PAGE" in str(e) and "MERGE_TIMEOUT" in str(e) and "cuda:3" in str(e)
+    assert "PARTIAL_RANGE" not in str(e)

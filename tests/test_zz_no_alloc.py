@@ -7,6 +7,8 @@ previous call's contents, so a stale partial or a counter left non-zero would sh
 balanced kernel for decode (R = 7) and verify (R = 35), with its two-pass and in-launch merges,
 and the per-head kernel with several splits per sequence (its in-launch merge counts arrivals in
 the array).  A call needing more scratch than the array holds is rejected before anything runs.
+Through the drop-in, a forked-branch table that would send the default call to cascade attention
+(which needs the module's workspace) runs the allocation-free path and allocates nothing.
 """
 
 import pytest
