@@ -1893,16 +1893,33 @@ __device__ __forceinline__ void merge_rows(const AttnParams& p, int hk, int b, c
 // The in-launch merge (decode rows, R <= 16).  Workgroups lean_grid, lean_grid + 1, ... of a
 // balanced launch merge the partials of (sequence b, KV head hk, query rows 4 rq .. 4 rq + 3),
 // one wave per row (two rows per wave, with half the workgroups, measured no faster): they wait
-// for (sequence, head)'s arrival counter to reach the part count, then merge with merge_rows.  Every XCD dispatches its workgroups in order, so these start only
-// on CUs that decode workgroups of lower index (which never wait) have left or never needed: a
-// merge workgroup waits only for workgroups that are already running.  The wait is bounded
+// for the arrival counter of (sequence, head, row group) to reach the part count, then merge with
+// merge_rows.  Every XCD dispatches its workgroups in order, so these start only on CUs that
+// decode workgroups of lower index (which never wait) have left or never needed: a merge
+// workgroup waits only for workgroups that are already running.  The wait is bounded
 // (kMergeSpinLimit polls; beyond it the wave flags PKV_STATUS_MERGE_TIMEOUT and leaves), so
-// every wave exits.  The counter's low 16 bits count arrived parts; each of the row groups'
-// workgroups adds 1 << 16 once it has read them, and the last to do so re-arms it at zero.
+// every wave exits.
+// Each row group has a counter of its own, which only its merge workgroup reads: a decode wave
+// adds 1 to the counter of every row group of each (sequence, head) it wrote a part of, and the
+// merge workgroup re-arms its counter with an atomic store of 0 (no read-modify-write, nothing
+// waits for it) as soon as the count is complete
+// (every part has arrived, so nothing adds to it again in this launch).  No atomic round trip
+// follows the merge: with one shared counter whose readers counted themselves out, the last
+// reader's fetch-and-add (and its re-arming store) sat between the merge and the end of the launch.
+// A merge that times out marks its counter with kMergePoison (parts still arriving add below it);
+// a later call's merge workgroup that finds the mark, or a count above the part count, flags
+// PKV_STATUS_MERGE_TIMEOUT and merges nothing until the counters are cleared.
 #ifndef PKV_MERGE_SPIN_LIMIT
 #define PKV_MERGE_SPIN_LIMIT (1 << 20)
 #endif
 constexpr int kMergeSpinLimit = PKV_MERGE_SPIN_LIMIT;
+constexpr int kMergePoison = 1 << 30;
+
+// Arrival counter of (segment gb = g * batch + b, head h of the group, row group rq).
+template <typename G>
+__device__ __forceinline__ int* merge_counter(const AttnParams& p, int gb, int h, int rq, int n_rq) {
+  return p.ws_cnt + ((gb * G::HG + h) * n_rq + rq) * p.cnt_stride;
+}
 
 template <typename G, int NCH>
 __device__ __forceinline__ void merge_workgroup(const AttnParams& p, const SeqTable<NCH>& st, int T1, int per,
@@ -1917,7 +1934,7 @@ __device__ __forceinline__ void merge_workgroup(const AttnParams& p, const SeqTa
   const int h = hk - g * G::HG;
   const SeqParts sp = seq_parts<NCH, G::TOK>(p, st, b, g * T1, per);
   if (sp.np <= 1) return;  // the sequence lies in one range: its output is written already
-  int* cnt = p.ws_cnt + ((g * p.batch + b) * G::HG + h) * p.cnt_stride;
+  int* cnt = merge_counter<G>(p, g * p.batch + b, h, rq, n_rq);
   // one poller per workgroup (every poll is a device-coherent load of a line that the arrivals
   // update; more pollers only queue behind each other and the arrivals), the others wait at the
   // barrier (ready_s: a word of the launch's LDS, which merge workgroups use for nothing else)
@@ -1925,30 +1942,27 @@ __device__ __forceinline__ void merge_workgroup(const AttnParams& p, const SeqTa
     int seen = 0;
     for (int i = 0; i < kMergeSpinLimit; ++i) {
       seen = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if ((seen & 0xffff) >= sp.np) break;
+      if (seen >= sp.np) break;
       __builtin_amdgcn_s_sleep(4);
     }
-    // n_rq or more readers already counted: a counter an earlier call's timed-out merge left
-    // armed (this call's own readers add only after they have merged), so its count is stale
-    const bool stale = (seen >> 16) >= n_rq;
-    *ready_s = (seen & 0xffff) >= sp.np && !stale ? 1 : (stale ? 2 : 0);
-    if (*ready_s != 1) flag_status(p.status, PKV_STATUS_MERGE_TIMEOUT);
+    // 1: every part is in; 2: a count an earlier call left (poisoned by its timeout, or above the
+    // part count); 0: timed out
+    const int state = seen == sp.np ? 1 : (seen > sp.np ? 2 : 0);
+    *ready_s = state;
+    if (state == 1)
+      __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      flag_status(p.status, PKV_STATUS_MERGE_TIMEOUT);
+    if (state == 0) __hip_atomic_fetch_or(cnt, kMergePoison, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
-  const int state = *ready_s;
-  const bool ready = state == 1;
   const int r0 = 4 * rq + int(threadIdx.x >> 6);
   const int rr[1] = {r0 < p.R ? r0 : -1};
-  if (ready && rr[0] >= 0)
+  if (*ready_s == 1 && rr[0] >= 0)
     merge_rows<G, true, 1, 64>(p, hk, b, rr, sp.np, [&](int part, int r) -> int64_t {
       const int slot = part == 0 ? sp.slot0 : 2 * (sp.w0 + part);
       return (int64_t(slot) * G::HG + h) * p.R + r;
     });
-  __syncthreads();  // every wave of this workgroup has read its parts
-  if (threadIdx.x == 0 && state != 2) {
-    const int prev = __hip_atomic_fetch_add(cnt, 1 << 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == (((n_rq - 1) << 16) | sp.np)) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
 }
 
 // Phase merge at the end of a segment (geometries with P > 1): the waves of phases 1 .. P-1
@@ -2297,18 +2311,19 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
       if (__any(ovf) && lane == 0) flag_status(p.status, PKV_STATUS_PARTIAL_RANGE);
     }
   }
-  if (p.two_pass || (pub_first < 0 && pub_last < 0)) return;
+  // verify rows (NT > 1: more than 16 rows per KV head) always merge in a second launch
+  if (NT > 1 || p.two_pass || (pub_first < 0 && pub_last < 0)) return;
   // In-launch merge: once this wave's partial stores have completed (device-coherent), count
-  // its arrival at each (sequence, head) it wrote a part of; a merge workgroup of this launch
-  // waits for the count to reach the part count.
+  // its arrival at each (sequence, head) it wrote a part of, on the counter of every row group
+  // (lanes [0, n_rq): the first segment's, [4, 4 + n_rq): the last's); a merge workgroup of this
+  // launch waits for its count to reach the part count.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the partial stores are device-visible
-  if (lane == 0) {
-    if (pub_first >= 0)
-      __hip_atomic_fetch_add(p.ws_cnt + (pub_first * G::HG + hg) * p.cnt_stride, 1, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-    if (pub_last >= 0)
-      __hip_atomic_fetch_add(p.ws_cnt + (pub_last * G::HG + hg) * p.cnt_stride, 1, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+  {
+    const int n_rq = (p.R + 3) / 4;
+    const int rq = lane & 3;
+    const int pub = lane < 4 ? pub_first : pub_last;
+    if (lane < 8 && rq < n_rq && pub >= 0)
+      __hip_atomic_fetch_add(merge_counter<G>(p, pub, hg, rq, n_rq), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -3474,7 +3489,10 @@ static int decode_attn(const char* fn, bool use_scratch, const void* q, int64_t 
     p.two_pass = fused && R <= 16 ? 0 : 1;
     // the counters 128 bytes apart where the counter region has room
     p.cnt_stride = 1;
-    while (p.cnt_stride < 32 && int64_t(batch) * n_kv * p.cnt_stride * 2 <= kMaxCounters) p.cnt_stride *= 2;
+    // one arrival counter per (sequence, KV head, group of 4 query rows) for the in-launch merge
+    const int64_t n_cnt = int64_t(batch) * n_kv * ((R + 3) / 4);
+    if (!p.two_pass && n_cnt > kMaxCounters) p.two_pass = 1;
+    while (p.cnt_stride < 32 && n_cnt * p.cnt_stride * 2 <= kMaxCounters) p.cnt_stride *= 2;
     p.lean_grid = grid;
     p.n_groups = n_kv / lean_heads_per_group(head_dim, n_kv);
     p.tok_elems = n_kv * head_dim;
