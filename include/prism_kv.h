@@ -140,8 +140,10 @@ size_t pkv_decode_workspace_bytes(int32_t batch, int32_t s_q, int32_t n_heads, i
  * PKV_DECODE_HEADS keeps fp32 partials.
  * workspace must hold pkv_decode_workspace_bytes() bytes and be
  * zero-filled before its first use; every call leaves it in that state again (its first 64 KiB
- * hold per-(sequence, KV head) arrival counters, so batch * n_kv <= 16384 when a sequence can
- * span more than one split).  Calls that share a workspace must be ordered (same
+ * hold the in-launch merges' arrival counters: per (sequence, KV head) for the per-head kernel,
+ * so batch * n_kv <= 16384 when a sequence can span more than one split, and per (sequence, KV
+ * head, group of 4 query rows) for the balanced kernel, which merges in a second launch when
+ * more than 16384 would be needed).  Calls that share a workspace must be ordered (same
  * stream).  It may be NULL when pkv_decode_workspace_bytes() returns 0.
  */
 int pkv_decode_attn(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
