@@ -172,6 +172,49 @@ def test_stale_merge_counters_are_flagged_then_cleared(gpu):
     assert not attn._reset_counters and torch.equal(na, good)
 
 
+def test_merge_timeout_marks_its_counter_until_the_counters_are_cleared(gpu):
+    # every arrival counter planted at -1 from the host, so each count stops one short of its part
+    # count: the merge workgroups wait out their bounded poll, flag PKV_STATUS_MERGE_TIMEOUT and
+    # mark their counters (bit 30); the next call's merge workgroups find a count above the part
+    # count and flag again without merging; reading the bit clears the counters, and the call
+    # after that is right.  Every kernel exits normally (the wait is bounded).
+    from prism_amd import attention as attn
+    cpu, dev = make_paged_case(gpu, batch=3, ctx=[3000, 17, 4100], page_size=256, n_kv=4, n_heads=28,
+                               head_dim=128, s_q=1, seed=22)
+    kw = dict(cache_seqlens=dev["cache_seqlens"], block_table=dev["block_table"], causal=True, two_pass=False,
+              grid=8)
+    good = prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], **kw)
+    torch.cuda.synchronize()
+    assert prism_amd.read_status(gpu) == 0
+    ref, _, _ = pa.flash_attn_with_kvcache_ref(cpu["q"], cpu["k_cache"], cpu["v_cache"],
+                                               cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"],
+                                               causal=True)
+    assert_attn_close(good, ref, "in-launch merge, 8 workgroups")
+    ws = attn._workspaces[(gpu.index or 0, torch.cuda.current_stream(gpu).cuda_stream)]
+    cnt = ws[:65536].view(torch.int32)
+    cnt.fill_(-1)
+    word = attn.status_tensor(gpu)
+    out = torch.full_like(good, float("nan"))
+    prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], out=out, **kw)
+    torch.cuda.synchronize()
+    assert int(word.item()) & prism_amd._lib.PKV_STATUS_MERGE_TIMEOUT
+    marked = cnt.cpu()
+    assert ((marked >= (1 << 30)) & (marked < (1 << 30) + 64)).any()   # a timed-out count, marked
+    assert not torch.equal(out, good)      # the split sequences' rows were left unwritten
+    word.zero_()
+    out2 = torch.full_like(good, float("nan"))
+    prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], out=out2, **kw)
+    torch.cuda.synchronize()
+    assert prism_amd.read_status(gpu) & prism_amd._lib.PKV_STATUS_MERGE_TIMEOUT   # the mark, seen
+    assert not torch.equal(out2, good)
+    torch.cuda.synchronize()
+    assert int(cnt.abs().sum()) == 0      # read_status cleared the counters
+    again = prism_amd.flash_attn_with_kvcache(dev["q"], dev["k_cache"], dev["v_cache"], **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(again, good)
+    assert prism_amd.read_status(gpu) == 0
+
+
 @pytest.mark.parametrize("prefix,s_q", [(2560, 5), (2048, 2)])
 def test_no_append_causal_verify_cuts_the_automatic_cascade_prefix(gpu, prefix, s_q):
     # 8 branches of one prompt on full shared pages, called the way flash_attn allows without an
