@@ -210,7 +210,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const NormParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) a[e] = a[e] + bb[e];
         v = pack8(a);
-        if (p.h_out) st16(p.h_out + r * p.h_stride + 8 * c, v);
+        if (p.h_out) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p.h_out + r * p.h_stride + 8 * c));
       }
       hv[k] = v;
       float f[8];
@@ -234,7 +234,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const NormParams p) {
       unpack8(wv[k], w);
 #pragma unroll
       for (int e = 0; e < 8; ++e) f[e] = f[e] * rs * w[e];
-      st16(p.out + r * p.o_stride + 8 * c, pack8(f));
+      __builtin_nontemporal_store(pack8(f), reinterpret_cast<u32x4*>(p.out + r * p.o_stride + 8 * c));
     }
   }
 }
@@ -269,7 +269,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const SiluParams p) {
       const float s = bf16r(gf[e] / (1.f + __expf(-gf[e])));
       o[e] = s * uf[e];
     }
-    st16(p.out + r * p.o_stride + 8 * c, pack8(o));
+    __builtin_nontemporal_store(pack8(o), reinterpret_cast<u32x4*>(p.out + r * p.o_stride + 8 * c));
   }
 }
 
