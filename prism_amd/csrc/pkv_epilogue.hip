@@ -73,6 +73,10 @@ __device__ __forceinline__ int64_t cache_row(const RopeParams& p, int b, int j) 
   return int64_t(pid) * p.page_stride + int64_t(slot & ((1 << p.log2_page) - 1)) * p.n_kv * p.head_dim;
 }
 
+__device__ __forceinline__ void stnt16(void* ptr, u32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(ptr));
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) void rope_qk_kernel(const RopeParams p) {
   constexpr int PC = HD / 16;  // pair chunks per head
@@ -100,7 +104,7 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(const RopeParams p) {
       const int hh = v / (HD / 8);
       const int c8 = v - hh * (HD / 8);
       const u32x4 x = ld16(row + (p.n_heads + p.n_kv + hh) * HD + 8 * c8);
-      if (crow >= 0) st16(p.v_cache + crow + hh * HD + 8 * c8, x);
+      if (crow >= 0) stnt16(p.v_cache + crow + hh * HD + 8 * c8, x);
       continue;
     }
     const int hh = i / PC;  // Q heads 0 .. n_heads-1, then K heads
@@ -145,18 +149,18 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(const RopeParams p) {
     const u32x4 v1 = pack8(o1), v2 = pack8(o2);
     if (!is_k) {
       uint16_t* dst = p.q_out + b * p.qo_sb + j * p.qo_ss + hh * p.qo_sh;
-      st16(dst + 8 * c, v1);
-      st16(dst + HD / 2 + 8 * c, v2);
+      stnt16(dst + 8 * c, v1);
+      stnt16(dst + HD / 2 + 8 * c, v2);
     } else {
       const int kh = hh - p.n_heads;
       if (p.k_out) {
         uint16_t* dst = p.k_out + b * p.ko_sb + j * p.ko_ss + kh * p.ko_sh;
-        st16(dst + 8 * c, v1);
-        st16(dst + HD / 2 + 8 * c, v2);
+        stnt16(dst + 8 * c, v1);
+        stnt16(dst + HD / 2 + 8 * c, v2);
       }
       if (crow >= 0) {
-        st16(p.k_cache + crow + kh * HD + 8 * c, v1);
-        st16(p.k_cache + crow + kh * HD + HD / 2 + 8 * c, v2);
+        stnt16(p.k_cache + crow + kh * HD + 8 * c, v1);
+        stnt16(p.k_cache + crow + kh * HD + HD / 2 + 8 * c, v2);
       }
     }
   }
