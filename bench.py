@@ -26,7 +26,10 @@ one (rope_decode_attention).
 lengths, rotary rows) at config 3's batch: DecodeBatch against the reference's refill.
 --workload decode-14B / decode-0.5B / decode-7B-tp4 run config 3's ragged batch at other model
 shapes.  --workload peak measures the streaming-read ceiling of the decode kernels' copy pattern
-(libpkv_probe.so) that the roofline's published 8 TB/s is checked against.
+(libpkv_probe.so) that the roofline's published 8 TB/s is checked against.  --workload
+tile-stamps reads the timeline of config 3's decode launch from the stamps build of the library
+(libprism_kv_stamps.so): when each workgroup starts, when each of its tiles lands, when its range
+ends and its parts arrive, and when the merges complete.
 """
 from __future__ import annotations
 
@@ -55,7 +58,7 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--workload", choices=["config2", "config3", "config4", "config5", "decode-14B", "decode-0.5B",
                                            "decode-7B-tp4", "long-decode", "long-decode-b1", "prefill-4096",
-                                           "epilogue", "tables", "peak"], default="config3")
+                                           "epilogue", "tables", "peak", "tile-stamps"], default="config3")
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = library choice)")
     ap.add_argument("--grid", type=int, default=0, help="workgroups of the balanced kernel (0 = one per CU)")
     ap.add_argument("--layers", type=int, default=0, help="layers (0 = the model's)")
@@ -64,6 +67,7 @@ def parse():
                     help="split-K merge of the per-head kernel: library choice, second launch, in-launch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=4, help="layers in the CPU baseline sample")
+    ap.add_argument("--stamp-calls", type=int, default=10, help="stamped calls read by --workload tile-stamps")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after timing, copy this many MiB of pages once (counter calibration)")
     return ap.parse_args()
@@ -586,6 +590,140 @@ def peak_bench(args, dev) -> dict:
     return res
 
 
+def tile_stamps_bench(args, dev) -> dict:
+    """Timeline of config 3's decode launch (decode_lean_kernel with its in-launch merge) from
+    libprism_kv_stamps.so: per-call time of both builds (graph replays), then eager calls whose
+    stamps are read back.  Times are us from the first decode workgroup's start (100 MHz clock).
+    Also bounds what a pool of tail tiles could gain on these measured timelines: the shortest
+    ranges of a static split (per - 1 tiles, as many as the tile count leaves) assigned to the
+    ranges that reach iteration k last (a claim made k tiles into the range, as a pool's copy
+    pipeline would need), or, as the bound, to the ranges that actually end last."""
+    import numpy as np
+    import torch
+
+    import prism_amd
+    from prism_amd import _lib, workloads
+    from prism_amd.build import LIB_PATH, STAMPS_LIB_PATH
+
+    if not STAMPS_LIB_PATH.exists():
+        raise RuntimeError(f"{STAMPS_LIB_PATH} is not built: run __graft_entry__.build() first")
+    w = workloads.config3(dev, seed=args.seed)
+    kv, L = w.kv, w.layers
+    outs = [torch.empty_like(q) for q in w.q]
+
+    def call(l):
+        prism_amd.flash_attn_with_kvcache(w.q[l], kv.k_caches[l], kv.v_caches[l], k=w.k[l], v=w.v[l],
+                                          cache_seqlens=w.cache_seqlens, block_table=w.block_table, causal=True,
+                                          out=outs[l])
+
+    def step():
+        for l in range(L):
+            call(l)
+
+    us_plain = time_graph(step, args, dev) * 1e3 / L
+    lib = _lib.use(STAMPS_LIB_PATH)
+    try:
+        import ctypes
+
+        lib.pkv_tile_stamp_words.restype = ctypes.c_int
+        lib.pkv_tile_stamps.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.pkv_tile_stamps_clear.argtypes = [ctypes.c_void_p]
+        us_stamped = time_graph(step, args, dev) * 1e3 / L
+        n_words = lib.pkv_tile_stamp_words()
+        host = torch.zeros(n_words, dtype=torch.int64).pin_memory()
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        calls = []
+        for i in range(4 + args.stamp_calls):
+            if lib.pkv_tile_stamps_clear(ctypes.c_void_p(stream)) != 0:
+                raise RuntimeError("pkv_tile_stamps_clear failed")
+            call(i % L)
+            if lib.pkv_tile_stamps(ctypes.c_void_p(host.data_ptr()), n_words * 8, ctypes.c_void_p(stream)) != 0:
+                raise RuntimeError("pkv_tile_stamps failed")
+            torch.cuda.synchronize()
+            if i >= 4:
+                calls.append(host.numpy().copy())
+        status = prism_amd.read_status(dev)
+    finally:
+        _lib.use(LIB_PATH)
+    if status:
+        raise RuntimeError(f"status word {status} after the stamped calls")
+
+    WG_WORDS, N_WG, N_MERGE = 32, 1024, 4096
+    per_call = []
+    for a in calls:
+        d = a[:N_WG * WG_WORDS].reshape(N_WG, WG_WORDS)
+        m = a[N_WG * WG_WORDS:N_WG * WG_WORDS + 4 * N_MERGE].reshape(N_MERGE, 4)
+        dec = np.nonzero(d[:, 0] > 0)[0]
+        t0 = d[dec, 0].min()
+        us = lambda x: (x - t0) / 100.0
+        full = [wg for wg in dec if d[wg, 3] > 0]
+        per = int(max(d[wg, 3] for wg in full))
+        rows = []
+        for wg in full:
+            n = int(d[wg, 3])
+            t = us(d[wg, 8:8 + min(n, 24)].astype(np.float64))
+            rows.append({"wg": int(wg), "n": n, "start": us(d[wg, 0]), "tiles": t, "end": us(d[wg, 1]),
+                         "arrival": us(d[wg, 2]) if d[wg, 2] else None, "segs": bin(int(d[wg, 4])).count("1"),
+                         "mask": int(d[wg, 4])})
+        mu = np.nonzero(m[:, 0] > 0)[0]
+        per_call.append({"rows": rows, "per": per, "grid": len(dec), "tiles": sum(r["n"] for r in rows),
+                         "merge_ready": us(m[mu, 1].max()) if len(mu) else None,
+                         "merge_done": us(m[mu, 2].max()) if len(mu) else None,
+                         "last_arrival": max((r["arrival"] for r in rows if r["arrival"] is not None), default=None)})
+
+    def med(xs):
+        return round(float(np.median(xs)), 2)
+
+    def pct(xs, q):
+        return round(float(np.percentile(xs, q)), 2)
+
+    first, plain, after_end, ends_by_seg, xcd_end = [], [], [], {}, {}
+    for c in per_call:
+        for r in c["rows"]:
+            t = r["tiles"]
+            first.append(t[0])
+            for j in range(1, len(t)):
+                (after_end if r["mask"] >> (j - 1) & 1 else plain).append(t[j] - t[j - 1])
+            ends_by_seg.setdefault(r["segs"], []).append(r["end"])
+            xcd_end.setdefault(r["wg"] % 8, []).append(r["end"])
+    # the tail-pool bound, per call: ranges of `per` tiles only
+    pool = {}
+    for c in per_call:
+        full = [r for r in c["rows"] if r["n"] == c["per"] and len(r["tiles"]) == c["per"]]
+        n_short = c["grid"] * c["per"] - c["tiles"]  # ranges a static split of per - 1 tiles leaves short
+        if c["per"] < 3 or n_short <= 0 or n_short >= len(full):
+            continue
+        T = np.array([r["tiles"] for r in full])
+        E = np.array([r["end"] for r in full])
+        end_short = T[:, -2] + (E - T[:, -1])  # the same range one tile shorter
+        for key, order in [(f"claim_at_tile_{k}", np.argsort(T[:, k])) for k in range(1, c["per"] - 2)] + \
+                          [("bound_slowest_known", np.argsort(E))]:
+            short, rest = order[-n_short:], order[:-n_short]
+            for cost in (0.3, 1.0):
+                new_last = max((E[rest] + cost).max(), end_short[short].max())
+                pool.setdefault(f"{key}_cost_{cost}", []).append(new_last - E.max())
+    return {
+        "us_per_call_plain": round(us_plain, 2), "us_per_call_stamped": round(us_stamped, 2),
+        "calls": len(per_call), "grid": per_call[0]["grid"], "tiles": per_call[0]["tiles"],
+        "tiles_per_range": per_call[0]["per"],
+        "start_spread_p90": med([pct([r["start"] for r in c["rows"]], 90) for c in per_call]),
+        "first_tile": {"median": med(first), "p90": pct(first, 90)},
+        "tile_interval": {"median": med(plain), "p90": pct(plain, 90)},
+        "tile_after_segment_end": {"median": med(after_end), "p90": pct(after_end, 90)} if after_end else None,
+        "range_end_by_segment_ends": {str(k): {"ranges": len(v), "median": med(v), "p90": pct(v, 90),
+                                               "max": round(float(np.max(v)), 2)}
+                                      for k, v in sorted(ends_by_seg.items())},
+        "range_end_median_by_xcd": {str(k): med(v) for k, v in sorted(xcd_end.items())},
+        "end_vs_first_tile_corr": round(float(np.corrcoef([r["end"] for c in per_call for r in c["rows"]],
+                                                          [r["tiles"][0] for c in per_call for r in c["rows"]])[0, 1]), 2),
+        "last_range_end": med([max(r["end"] for r in c["rows"]) for c in per_call]),
+        "last_arrival": med([c["last_arrival"] for c in per_call if c["last_arrival"] is not None]),
+        "last_merge_ready": med([c["merge_ready"] for c in per_call if c["merge_ready"] is not None]),
+        "last_merge_done": med([c["merge_done"] for c in per_call if c["merge_done"] is not None]),
+        "tail_pool_change_of_last_range_end_us": {k: med(v) for k, v in pool.items()},
+    }
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -643,6 +781,20 @@ def main() -> int:
                          "frac": round(best / HBM_PEAK_GBS, 4), "traffic": None,
                          "kernel": "stream_read_kernel (libpkv_probe.so); HIP events around K launches",
                          "bytes_per_call": res["hbm_nt"]["bytes"], "avg_call_us": res["hbm_nt"]["us"]},
+            "detail": res,
+        }
+        print(json.dumps(result), flush=True)
+        return 0
+    if args.workload == "tile-stamps":
+        res = tile_stamps_bench(args, dev)
+        result = {
+            "metric": "config-3 decode call timeline (decode_lean_kernel + in-launch merge), us from the first "
+                      "workgroup's start",
+            "value": res["last_merge_done"], "unit": "us", "n_gpus": 1, "steps": args.stamp_calls, "warmup": 4,
+            "ms_per_step": round(res["us_per_call_stamped"] / 1e3, 5), "higher_is_better": False, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "tile-stamps: config 3's call (layer i of the 28, eager) on the stamps build "
+                                   "(libprism_kv_stamps.so)", "seed": args.seed},
             "detail": res,
         }
         print(json.dumps(result), flush=True)

@@ -175,6 +175,16 @@ def load() -> ctypes.CDLL:
         return lib
 
 
+def use(path: Path) -> ctypes.CDLL:
+    """Load another build of the library (bench.py's timeline-stamp variant) in place of the one
+    loaded so far: every later call of this package goes to it."""
+    global _lib, LIB_PATH
+    with _lock:
+        _lib = None
+        LIB_PATH = Path(path)
+    return load()
+
+
 def check(rc: int, what: str) -> None:
     if rc != PKV_OK:
         msg = load().pkv_last_error().decode(errors="replace")

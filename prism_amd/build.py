@@ -5,6 +5,9 @@ Usage: python -m prism_amd.build   (or prism_amd.build.build() from Python).
 Every .hip file under prism_amd/csrc is compiled by hipcc for gfx950 into one object each (in
 parallel), then linked into prism_amd/libprism_kv.so.  The .so is what the ctypes loader
 (prism_amd/_lib.py) opens; it is git-ignored but travels with the source tree to a GPU host.
+Two more libraries come out of the same run: libpkv_probe.so (the streaming-read probe of
+bench.py --workload peak) and libprism_kv_stamps.so (the kernels with decode_lean_kernel's
+timeline stamps, for bench.py --workload tile-stamps).
 """
 from __future__ import annotations
 
@@ -20,6 +23,10 @@ CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libprism_kv.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 PROBE_LIB_PATH = PKG_DIR / "libpkv_probe.so"
+# the same library with decode_lean_kernel's timeline stamps (-DPKV_TILE_STAMPS): only
+# bench.py --workload tile-stamps loads it
+STAMPS_LIB_PATH = PKG_DIR / "libprism_kv_stamps.so"
+STAMPS_SOURCE = "pkv_attention.hip"
 BUILD_DIR = PKG_DIR / "_build"
 ARCH = "gfx950"
 
@@ -75,6 +82,9 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     objs = [BUILD_DIR / (s.stem + ".o") for s in sources]
     cmds = [[hipcc, *HIPCC_FLAGS, *extra, "-c", str(s), "-o", str(o)] for s, o in zip(sources, objs)]
+    stamps_obj = BUILD_DIR / (Path(STAMPS_SOURCE).stem + "_stamps.o")
+    cmds.insert(1, [hipcc, *HIPCC_FLAGS, *extra, "-DPKV_TILE_STAMPS", "-c", str(CSRC / STAMPS_SOURCE), "-o",
+                    str(stamps_obj)])
     workers = min(len(cmds), max(1, (os.cpu_count() or 2) // 2), 8)
     with cf.ThreadPoolExecutor(workers) as ex:
         for cmd, fut in zip(cmds, [ex.submit(_run, c) for c in cmds]):
@@ -86,6 +96,12 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH}")
+    stamps_objs = [stamps_obj if o.name == Path(STAMPS_SOURCE).stem + ".o" else o for o in objs]
+    tmp = STAMPS_LIB_PATH.with_suffix(".so.tmp")
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, stamps_objs)])
+    os.replace(tmp, STAMPS_LIB_PATH)
+    if verbose:
+        print(f"built {STAMPS_LIB_PATH}")
     # the bandwidth probe bench.py --workload peak runs: its own library, outside the paged-KV ABI
     probe_src = PKG_DIR / "csrc_probe" / "pkv_probe.hip"
     probe_tmp = PROBE_LIB_PATH.with_suffix(".so.tmp")

@@ -1915,6 +1915,28 @@ __device__ __forceinline__ void merge_rows(const AttnParams& p, int hk, int b, c
 constexpr int kMergeSpinLimit = PKV_MERGE_SPIN_LIMIT;
 constexpr int kMergePoison = 1 << 30;
 
+#ifdef PKV_TILE_STAMPS
+// Timeline instrumentation of decode_lean_kernel (decode rows), compiled only into the stamps
+// variant of the library (libprism_kv_stamps.so, built with -DPKV_TILE_STAMPS): s_memrealtime
+// readings (a 100 MHz clock) of every decode workgroup's start, each tile's landing (after the
+// wait and barrier at the top of its iteration; kept in lanes of one register, so no memory
+// operation enters the tile loop), the end of its range and its arrival, and of every merge
+// workgroup's start, count complete and merge done.  Decode workgroup w: words w * 32 + [0 start,
+// 1 range end, 2 arrival counted, 3 tiles, 4 mask of segment-end iterations, 8 + j tile j
+// landed (j < 24)]; merge workgroup m: words kStampMerge0 + 4 m + [0 start, 1 count complete,
+// 2 merge stored, 3 parts].  Read by pkv_tile_stamps, cleared by pkv_tile_stamps_clear.
+constexpr int kStampWgs = 1024, kStampWgWords = 32, kStampMerges = 4096;
+constexpr int kStampMerge0 = kStampWgs * kStampWgWords;
+constexpr int kStampWords = kStampMerge0 + 4 * kStampMerges;
+__device__ uint64_t g_tile_stamps[kStampWords];
+__device__ __forceinline__ void stamp_now(int i) {
+  if (i < kStampWords) g_tile_stamps[i] = __builtin_amdgcn_s_memrealtime();
+}
+__device__ __forceinline__ void stamp_value(int i, uint64_t v) {
+  if (i < kStampWords) g_tile_stamps[i] = v;
+}
+#endif
+
 // Arrival counter of (segment gb = g * batch + b, head h of the group, row group rq).
 template <typename G>
 __device__ __forceinline__ int* merge_counter(const AttnParams& p, int gb, int h, int rq, int n_rq) {
@@ -1935,6 +1957,9 @@ __device__ __forceinline__ void merge_workgroup(const AttnParams& p, const SeqTa
   const SeqParts sp = seq_parts<NCH, G::TOK>(p, st, b, g * T1, per);
   if (sp.np <= 1) return;  // the sequence lies in one range: its output is written already
   int* cnt = merge_counter<G>(p, g * p.batch + b, h, rq, n_rq);
+#ifdef PKV_TILE_STAMPS
+  if (threadIdx.x == 0) stamp_now(kStampMerge0 + 4 * m);
+#endif
   // one poller per workgroup (every poll is a device-coherent load of a line that the arrivals
   // update; more pollers only queue behind each other and the arrivals), the others wait at the
   // barrier (ready_s: a word of the launch's LDS, which merge workgroups use for nothing else)
@@ -1949,6 +1974,9 @@ __device__ __forceinline__ void merge_workgroup(const AttnParams& p, const SeqTa
     // part count); 0: timed out
     const int state = seen == sp.np ? 1 : (seen > sp.np ? 2 : 0);
     *ready_s = state;
+#ifdef PKV_TILE_STAMPS
+    stamp_now(kStampMerge0 + 4 * m + 1);
+#endif
     if (state == 1)
       __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     else
@@ -1963,6 +1991,14 @@ __device__ __forceinline__ void merge_workgroup(const AttnParams& p, const SeqTa
       const int slot = part == 0 ? sp.slot0 : 2 * (sp.w0 + part);
       return (int64_t(slot) * G::HG + h) * p.R + r;
     });
+#ifdef PKV_TILE_STAMPS
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the merged rows are stored
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    stamp_now(kStampMerge0 + 4 * m + 2);
+    stamp_value(kStampMerge0 + 4 * m + 3, uint64_t(sp.np));
+  }
+#endif
 }
 
 // Phase merge at the end of a segment (geometries with P > 1): the waves of phases 1 .. P-1
@@ -2054,6 +2090,10 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   const bool leader = ph == 0;
   const int li = lane & 15;
   const int lq = lane >> 4;
+#ifdef PKV_TILE_STAMPS
+  if (threadIdx.x == 0 && int(blockIdx.x) < min(p.lean_grid, kStampWgs)) stamp_now(int(blockIdx.x) * kStampWgWords);
+  uint64_t st_tiles = 0, st_mask = 0;  // lane 8 + j: tile j's landing; bit j: iteration j ends a segment
+#endif
 
   SeqTable<NCH> st;
   seq_table<NCH, TOK>(p, st);
@@ -2136,6 +2176,9 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     else
       wait_vmcnt_at_most(16 + (q_area_copy<G, kRope>(p, dB, kQInLds) ? kQCopies : 0) + stores_prev + stores_prev2);
     raw_barrier();  // ... and every other wave's
+#ifdef PKV_TILE_STAMPS
+    if (j < 24) st_tiles = lane == 8 + j ? __builtin_amdgcn_s_memrealtime() : st_tiles;
+#endif
     if (__builtin_expect(j == 0 || d.T0 == p.k0, 0)) {
       // a segment starts: its Q operand, row limits and a fresh softmax state
       if constexpr (kQInLds) {
@@ -2184,6 +2227,9 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
     raw_barrier();                       // nobody reads this buffer any more
     const bool seg_end = !(j + 1 < n && d.T0 + TOK < d.L);
+#ifdef PKV_TILE_STAMPS
+    if (seg_end && j < 64) st_mask |= 1ull << j;
+#endif
     // With phases, a segment end merges the phase states in this buffer first, and tile j + 2's
     // copies wait until that is done.
     const bool defer = G::P > 1 && seg_end;
@@ -2311,6 +2357,17 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
       if (__any(ovf) && lane == 0) flag_status(p.status, PKV_STATUS_PARTIAL_RANGE);
     }
   }
+#ifdef PKV_TILE_STAMPS
+  const int st_base = int(blockIdx.x) * kStampWgWords;
+  if (int(blockIdx.x) < kStampWgs) {
+    if (threadIdx.x == 0) {
+      stamp_now(st_base + 1);
+      stamp_value(st_base + 3, uint64_t(n));
+      stamp_value(st_base + 4, st_mask);
+    }
+    if (w == 0 && lane >= 8 && lane < 8 + min(n, 24)) stamp_value(st_base + lane, st_tiles);
+  }
+#endif
   // verify rows (NT > 1: more than 16 rows per KV head) always merge in a second launch
   if (NT > 1 || p.two_pass || (pub_first < 0 && pub_last < 0)) return;
   // In-launch merge: once this wave's partial stores have completed (device-coherent), count
@@ -2325,6 +2382,9 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     if (lane < 8 && rq < n_rq && pub >= 0)
       __hip_atomic_fetch_add(merge_counter<G>(p, pub, hg, rq, n_rq), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+#ifdef PKV_TILE_STAMPS
+  if (threadIdx.x == 0 && int(blockIdx.x) < kStampWgs) stamp_now(st_base + 2);
+#endif
 }
 
 // Two-pass merge (PKV_DECODE_TWO_PASS) of the partials a decode_lean_kernel launch of `grid`
@@ -3711,3 +3771,24 @@ extern "C" int pkv_prefill_attn(const void* q, int64_t q_sb, int64_t q_ss, int64
     launch_prefill_hd<64>(p, batch, s);
   return check_launch(fn);
 }
+
+#ifdef PKV_TILE_STAMPS
+// Stamps variant only (libprism_kv_stamps.so; bench.py --workload tile-stamps): copy the current
+// device's stamp words (kStampWords uint64) to host memory `dst` on `stream`, or zero them.  No
+// counterpart in the reference: timeline instrumentation of decode_lean_kernel.
+extern "C" int pkv_tile_stamps(void* dst, size_t bytes, void* stream) {
+  void* ptr = nullptr;
+  if (bytes < sizeof(uint64_t) * pkv::kStampWords) return PKV_EINVAL;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(pkv::g_tile_stamps)) != hipSuccess) return PKV_EHIP;
+  return hipMemcpyAsync(dst, ptr, sizeof(uint64_t) * pkv::kStampWords, hipMemcpyDeviceToHost,
+                        static_cast<hipStream_t>(stream)) == hipSuccess ? PKV_OK : PKV_EHIP;
+}
+extern "C" int pkv_tile_stamps_clear(void* stream) {
+  void* ptr = nullptr;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(pkv::g_tile_stamps)) != hipSuccess) return PKV_EHIP;
+  return hipMemsetAsync(ptr, 0, sizeof(uint64_t) * pkv::kStampWords, static_cast<hipStream_t>(stream)) == hipSuccess
+             ? PKV_OK
+             : PKV_EHIP;
+}
+extern "C" int pkv_tile_stamp_words(void) { return pkv::kStampWords; }
+#endif
