@@ -68,6 +68,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=4, help="layers in the CPU baseline sample")
     ap.add_argument("--stamp-calls", type=int, default=10, help="stamped calls read by --workload tile-stamps")
+    ap.add_argument("--stamps-of", choices=["config3", "config2", "decode-0.5B", "decode-7B-tp4"], default="config3",
+                    help="the decode workload --workload tile-stamps records")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after timing, copy this many MiB of pages once (counter calibration)")
     return ap.parse_args()
@@ -591,7 +593,8 @@ def peak_bench(args, dev) -> dict:
 
 
 def tile_stamps_bench(args, dev) -> dict:
-    """Timeline of config 3's decode launch (decode_lean_kernel with its in-launch merge) from
+    """Timeline of a decode launch (decode_lean_kernel with its in-launch merge; config 3 unless
+    --stamps-of names another decode workload) from
     libprism_kv_stamps.so: per-call time of both builds (graph replays), then eager calls whose
     stamps are read back.  Times are us from the first decode workgroup's start (100 MHz clock).
     Also bounds what a pool of tail tiles could gain on these measured timelines: the shortest
@@ -607,7 +610,12 @@ def tile_stamps_bench(args, dev) -> dict:
 
     if not STAMPS_LIB_PATH.exists():
         raise RuntimeError(f"{STAMPS_LIB_PATH} is not built: run __graft_entry__.build() first")
-    w = workloads.config3(dev, seed=args.seed)
+    if args.stamps_of.startswith("decode-"):
+        w = workloads.ragged_decode(args.stamps_of[len("decode-"):], dev, seed=args.seed)
+    elif args.stamps_of == "config2" and args.batch:
+        w = workloads.config2(dev, seed=args.seed, batch=args.batch)
+    else:
+        w = getattr(workloads, args.stamps_of)(dev, seed=args.seed)
     kv, L = w.kv, w.layers
     outs = [torch.empty_like(q) for q in w.q]
 
@@ -788,13 +796,13 @@ def main() -> int:
     if args.workload == "tile-stamps":
         res = tile_stamps_bench(args, dev)
         result = {
-            "metric": "config-3 decode call timeline (decode_lean_kernel + in-launch merge), us from the first "
-                      "workgroup's start",
+            "metric": f"{args.stamps_of} decode call timeline (decode_lean_kernel + in-launch merge), us from the "
+                      "first workgroup's start",
             "value": res["last_merge_done"], "unit": "us", "n_gpus": 1, "steps": args.stamp_calls, "warmup": 4,
             "ms_per_step": round(res["us_per_call_stamped"] / 1e3, 5), "higher_is_better": False, "scaling": "weak",
             "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-            "config": {"workload": "tile-stamps: config 3's call (layer i of the 28, eager) on the stamps build "
-                                   "(libprism_kv_stamps.so)", "seed": args.seed},
+            "config": {"workload": f"tile-stamps: {args.stamps_of}'s call (layer i, eager) on the stamps build "
+                                   "(libprism_kv_stamps.so)", "seed": args.seed, "batch": args.batch or None},
             "detail": res,
         }
         print(json.dumps(result), flush=True)

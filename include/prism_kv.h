@@ -26,7 +26,8 @@
  *     (engine/kv_cache.py:37-46); `*_page_stride` is the element distance between pages.
  *   - Strides are in elements (16-bit words) unless the name says _bytes.  The innermost
  *     (head_dim) dimension must be contiguous and every row 16-byte aligned.
- *   - block_table is int32 [batch, bt_stride] (only the first max_blocks columns are read);
+ *   - block_table is int32 [batch, bt_stride] (only the first max_blocks columns are read;
+ *     max_blocks * page_size, the keys a sequence may hold, is at most 2^27);
  *     cache_seqlens is int32 [batch] and holds each sequence's length BEFORE the append
  *     (engine/kv_cache.py:123-153).
  *   - `status` (nullable) is a device int32 the kernels OR error bits into instead of

@@ -66,6 +66,10 @@ int validate_paged(const char* fn, const void* k_cache, const void* v_cache, int
     return fail(PKV_EINVAL, "%s: head_dim %d unsupported (64 or 128)", fn, head_dim);
   if (!is_pow2(page_size) || page_size < 16)
     return fail(PKV_EINVAL, "%s: page_size %d must be a power of two >= 16", fn, page_size);
+  // every kernel indexes a sequence's keys in 32 bits, and the balanced decode split counts tiles
+  // with single-precision arithmetic: at most 2^27 keys per sequence
+  if (int64_t(max_blocks) * page_size > (int64_t(1) << 27))
+    return fail(PKV_EINVAL, "%s: max_blocks %d x page_size %d > 2^27 keys per sequence", fn, max_blocks, page_size);
   if (bt_stride < max_blocks)
     return fail(PKV_EINVAL, "%s: bt_stride %lld < max_blocks %d", fn, (long long)bt_stride, max_blocks);
   if (page_stride < int64_t(page_size) * n_kv * head_dim || (page_stride % 8) != 0)

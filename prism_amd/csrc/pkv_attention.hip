@@ -884,7 +884,10 @@ __global__ __launch_bounds__(512) void combine_kernel(const AttnParams p) {
 // one tile, which yields its zero output); the tiles of all sequences, in sequence order, form
 // one list of T tiles, and persistent workgroup w of G owns the contiguous range
 // [w * per, (w + 1) * per), per = ceil(T / G).  Every workgroup streams the same bytes to within
-// one tile, whatever the context lengths.  The sequences a range touches are its segments; a
+// one tile, whatever the context lengths.  (For decode rows of a few sequences, and wherever a
+// head's keys are split over phase waves, the host picks a variant that cuts each sequence into
+// ceil(t_b / per) ranges of its own when those fit the grid: aligned_range.)  The sequences a
+// range touches are its segments; a
 // segment holding a whole sequence writes the bf16 output directly, the others (at most the
 // first and the last segment of a range) write an fp32 partial (m, l, O) to workspace slot
 // 2w (first segment of the range) or 2w + 1 (last), merged by combine_lean_kernel.
@@ -1712,28 +1715,101 @@ __device__ __forceinline__ void ws_store_partial(__amdgpu_buffer_rsrc_t rs, uint
   if (with_lse) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, lse), rs, int(lse_off), 0, POL);
 }
 
-// Parts of sequence b in a balanced launch: the ranges w0..w1 its tiles fall in (per tiles each)
-// and the workspace slot of part 0 (range w0 holds b in its first segment only when b starts at
-// w0's first tile; every later part is its range's first segment, slot 2w).
+// Sequence-aligned split.  A range that holds the end of one sequence and the start of the next
+// pays a second segment (its epilogue and partial, the next sequence's Q and limits) and ends
+// ~2.4 us after a one-segment range at 7B decode, B = 8 (timeline stamps), so the merge waits for
+// it.  When ceil(t_b / per) ranges per sequence (t_b tiles, per = ceil(T / G) as in the plain
+// split), over every head group, fit the G workgroups, the launch uses those instead: sequence b's
+// tiles in ranges of per tiles (the last shorter), ranges of head group g numbered after those of
+// group g - 1, no range crossing a sequence.  Otherwise (7B decode at B = 32, 14B) the plain
+// contiguous split stays.  RangeTable: lane l of register q holds the first aligned range of
+// sequence 64q + l within its head group; rtotal is the aligned ranges of one head group.
+template <int NCH>
+struct RangeTable {
+  int rfirst[NCH];
+  int rtotal;
+};
+
+template <int NCH, int TOK>
+__device__ __forceinline__ void range_table(const AttnParams& p, const SeqTable<NCH>& st, int per,
+                                            RangeTable<NCH>& rt) {
+  const int lane = threadIdx.x & 63;
+  // ceil(t / per) from a float reciprocal: t < 2^22 tiles, so the estimate's floor is within one
+  // of t / per from below, and two steps make it exact (shorter than an integer division on the
+  // launch's critical path, before the first block-table read)
+  const float inv = 1.f / float(per);
+  int base = 0;
+#pragma unroll
+  for (int q = 0; q < NCH; ++q) {
+    const int t = 64 * q + lane < p.batch ? seq_tiles<TOK>(p, st.L[q]) : 0;
+    int r = int(float(t) * inv);
+    r += r * per < t ? 1 : 0;
+    r += r * per < t ? 1 : 0;
+    const int incl = base + wave_incl_scan(r);
+    rt.rfirst[q] = incl - r;
+    base = __builtin_amdgcn_readlane(incl, 63);
+  }
+  rt.rtotal = base;
+}
+
+// Tiles [s, e) of workgroup w under the aligned split (s == e past its last range).  Every real
+// sequence has at least one range, so the ranges' first indices rise strictly over the sequences
+// and the sequence of range w is the last one whose first range is <= w.
+template <int NCH, int TOK>
+__device__ __forceinline__ void aligned_range(const AttnParams& p, const SeqTable<NCH>& st, const RangeTable<NCH>& rt,
+                                              int T1, int per, int w, int& s, int& e) {
+  const int lane = threadIdx.x & 63;
+  const int g = w / rt.rtotal;
+  const int wg = w - g * rt.rtotal;
+  int first = 0, L = 0, r0 = 0;
+#pragma unroll
+  for (int q = 0; q < NCH; ++q) {
+    const uint64_t m = __ballot(64 * q + lane < p.batch && rt.rfirst[q] <= wg);
+    if (m) {
+      const int pos = 63 - __clzll(m);
+      first = __builtin_amdgcn_readlane(st.first[q], pos);
+      L = __builtin_amdgcn_readlane(st.L[q], pos);
+      r0 = __builtin_amdgcn_readlane(rt.rfirst[q], pos);
+    }
+  }
+  s = g * T1 + first + (wg - r0) * per;
+  e = min(s + per, g * T1 + first + seq_tiles<TOK>(p, L));
+  if (g >= p.n_groups) e = s;
+}
+
+// Parts of sequence b (head group g) in a balanced launch: np ranges from w0 on, and the
+// workspace slot of part 0.  Plain split: the ranges its tiles fall in (per tiles each); range w0
+// holds b in its first segment only when b starts at w0's first tile, and every later part is
+// its range's first segment, slot 2w.  Aligned split: ceil(t_b / per) ranges of their own, each
+// a first segment (slot 2w).
 struct SeqParts {
   int np, w0, slot0;
 };
 
 template <int NCH, int TOK>
-__device__ __forceinline__ SeqParts seq_parts(const AttnParams& p, const SeqTable<NCH>& st, int b, int base, int per) {
-  int first = 0, L = 0;
+__device__ __forceinline__ SeqParts seq_parts(const AttnParams& p, const SeqTable<NCH>& st, const RangeTable<NCH>& rt,
+                                              bool aligned, int b, int g, int T1, int per) {
+  int first = 0, L = 0, r0 = 0;
 #pragma unroll
   for (int q = 0; q < NCH; ++q) {
     if (q == (b >> 6)) {
       first = __builtin_amdgcn_readlane(st.first[q], b & 63);
       L = __builtin_amdgcn_readlane(st.L[q], b & 63);
+      r0 = __builtin_amdgcn_readlane(rt.rfirst[q], b & 63);
     }
   }
-  first += base;  // the group's first tile
   SeqParts sp;
-  sp.w0 = first / per;
-  sp.np = (first + seq_tiles<TOK>(p, L) - 1) / per - sp.w0 + 1;
-  sp.slot0 = 2 * sp.w0 + (first != sp.w0 * per ? 1 : 0);
+  const int t = seq_tiles<TOK>(p, L);
+  if (aligned) {
+    sp.w0 = g * rt.rtotal + r0;
+    sp.np = (t + per - 1) / per;
+    sp.slot0 = 2 * sp.w0;
+  } else {
+    first += g * T1;  // the group's first tile
+    sp.w0 = first / per;
+    sp.np = (first + t - 1) / per - sp.w0 + 1;
+    sp.slot0 = 2 * sp.w0 + (first != sp.w0 * per ? 1 : 0);
+  }
   return sp;
 }
 
@@ -1944,7 +2020,8 @@ __device__ __forceinline__ int* merge_counter(const AttnParams& p, int gb, int h
 }
 
 template <typename G, int NCH>
-__device__ __forceinline__ void merge_workgroup(const AttnParams& p, const SeqTable<NCH>& st, int T1, int per,
+__device__ __forceinline__ void merge_workgroup(const AttnParams& p, const SeqTable<NCH>& st,
+                                                const RangeTable<NCH>& rt, bool aligned, int T1, int per,
                                                 int* ready_s) {
   const int m = int(blockIdx.x) - p.lean_grid;
   const int n_rq = (p.R + 3) / 4;
@@ -1954,7 +2031,7 @@ __device__ __forceinline__ void merge_workgroup(const AttnParams& p, const SeqTa
   if (b >= p.batch) return;
   const int g = hk / G::HG;
   const int h = hk - g * G::HG;
-  const SeqParts sp = seq_parts<NCH, G::TOK>(p, st, b, g * T1, per);
+  const SeqParts sp = seq_parts<NCH, G::TOK>(p, st, rt, aligned, b, g, T1, per);
   if (sp.np <= 1) return;  // the sequence lies in one range: its output is written already
   int* cnt = merge_counter<G>(p, g * p.batch + b, h, rq, n_rq);
 #ifdef PKV_TILE_STAMPS
@@ -2063,8 +2140,9 @@ __device__ __forceinline__ void phase_merge(char* buf, float (&m_run)[NT], float
   }
 }
 
-template <int NT, int NCH, bool CASCADE_SUFFIX, typename G, bool ROPE = false>
+template <int NT, int NCH, bool CASCADE_SUFFIX, typename G, bool ROPE = false, bool ALIGN = false>
 __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p) {
+  static_assert(!ALIGN || (NT == 1 && !CASCADE_SUFFIX), "the aligned split is for decode rows");
   constexpr int HD = G::HD;
   constexpr int DPL = HD / 16;
   constexpr int KK = HD / 32;
@@ -2100,12 +2178,25 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
   const int T1 = st.total;  // tiles of one head group
   const int total = T1 * p.n_groups;
   const int per = (total + p.lean_grid - 1) / p.lean_grid;
+  // an instantiation of its own (the host's choice): its prologue code costs the launches that
+  // keep the plain split 0.3-0.4 us
+  RangeTable<NCH> rt;
+  bool aligned = false;
+  if constexpr (ALIGN) {
+    range_table<NCH, TOK>(p, st, per, rt);
+    aligned = rt.rtotal * p.n_groups <= p.lean_grid;
+  }
   if (int(blockIdx.x) >= p.lean_grid) {
-    if constexpr (NT == 1) merge_workgroup<G, NCH>(p, st, T1, per, reinterpret_cast<int*>(lds));
+    if constexpr (NT == 1) merge_workgroup<G, NCH>(p, st, rt, aligned, T1, per, reinterpret_cast<int*>(lds));
     return;
   }
-  const int s = min(int(blockIdx.x) * per, total);
-  const int e = min(s + per, total);
+  int s, e;
+  if (aligned) {
+    aligned_range<NCH, TOK>(p, st, rt, T1, per, int(blockIdx.x), s, e);
+  } else {
+    s = min(int(blockIdx.x) * per, total);
+    e = min(s + per, total);
+  }
   if (s >= e) return;
   const int n = e - s;
 
@@ -2393,7 +2484,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
 // where 16-wave ones ran one at a time); only sequences whose tiles span more than one range have
 // partials, and in a cascade launch every sequence has the prefix pass's parts as well.
 template <typename G>
-__global__ __launch_bounds__(512) void combine_lean_kernel(const AttnParams p, int grid) {
+__global__ __launch_bounds__(512) void combine_lean_kernel(const AttnParams p, int grid, int align) {
   const int hk = blockIdx.x;  // KV head; its group's tiles follow those of the groups before it
   const int g = hk / G::HG;
   const int h = hk - g * G::HG;  // head within the group (the partials hold HG per slot)
@@ -2406,17 +2497,20 @@ __global__ __launch_bounds__(512) void combine_lean_kernel(const AttnParams p, i
   // seq_table (same clamp), one 64-sequence chunk at a time
   const int cap = p.max_blocks << p.log2_page;
   const int s_new = p.has_new ? p.s_q : 0;
-  int first = 0, L = 0, total = 0;
-#pragma unroll 1
-  for (int q0 = 0; q0 < p.batch; q0 += 64) {
-    const int bb = q0 + lane;
+  auto tiles_of_lane = [&](int bb, int& Lb) {
     int c = bb < p.batch ? p.seqlens[bb] : 0;
-    int Lb = c + s_new;
+    Lb = c + s_new;
     if (c < 0 || Lb > cap) {
       c = min(max(c, 0), cap);
       Lb = min(c + s_new, cap);
     }
-    const int n = bb < p.batch ? seq_tiles<G::TOK>(p, Lb) : 0;
+    return bb < p.batch ? seq_tiles<G::TOK>(p, Lb) : 0;
+  };
+  int first = 0, L = 0, total = 0;
+#pragma unroll 1
+  for (int q0 = 0; q0 < p.batch; q0 += 64) {
+    int Lb;
+    const int n = tiles_of_lane(q0 + lane, Lb);
     const int incl = total + wave_incl_scan(n);
     if (b >= q0 && b < q0 + 64) {
       first = __builtin_amdgcn_readlane(incl - n, b - q0);
@@ -2425,15 +2519,34 @@ __global__ __launch_bounds__(512) void combine_lean_kernel(const AttnParams p, i
     total = __builtin_amdgcn_readlane(incl, 63);
   }
   const int per = (total * p.n_groups + grid - 1) / grid;
-  first += g * total;
-  const int w0 = first / per;
-  const int np = (first + seq_tiles<G::TOK>(p, L) - 1) / per - w0 + 1;
+  // the split the decode launch chose (range_table, aligned_range): a second pass over the lengths
+  // for the aligned split's range counts
+  int r0 = 0, rtotal = 0;
+#pragma unroll 1
+  for (int q0 = 0; q0 < (align ? p.batch : 0); q0 += 64) {
+    int Lb;
+    const int r = (tiles_of_lane(q0 + lane, Lb) + per - 1) / per;
+    const int incl = rtotal + wave_incl_scan(r);
+    if (b >= q0 && b < q0 + 64) r0 = __builtin_amdgcn_readlane(incl - r, b - q0);
+    rtotal = __builtin_amdgcn_readlane(incl, 63);
+  }
+  const int t_b = seq_tiles<G::TOK>(p, L);
+  int w0, np, slot0;
+  if (align && rtotal * p.n_groups <= grid) {
+    w0 = g * rtotal + r0;
+    np = (t_b + per - 1) / per;
+    slot0 = 2 * w0;
+  } else {
+    first += g * total;
+    w0 = first / per;
+    np = (first + t_b - 1) / per - w0 + 1;
+    // the first range holds b in its first segment only if b starts exactly at the range start
+    slot0 = 2 * w0 + (first != w0 * per ? 1 : 0);
+  }
   // cascade: the prefix pass's S parts first, then the sequence's suffix partial(s)
   const int S = p.cascade_splits;
   if (np <= 1 && S == 0) return;
   const int n_parts = S + (np <= 1 ? 1 : np);
-  // the first range holds b in its first segment only if b starts exactly at the range start
-  const int slot0 = 2 * w0 + (first != w0 * per ? 1 : 0);
   const int rr[1] = {r};
   merge_rows<G, false, 1, 32>(p, hk, b, rr, n_parts, [&](int part, int r) -> int64_t {
     int slot;
@@ -3177,14 +3290,21 @@ static int lean_grid(int32_t flags) {
 // The launch's workgroups: `grid` that decode, then (in-launch merge) one per (sequence, KV head,
 // group of 4 query rows) that merge.
 template <int NT, bool CS, typename G>
-static void launch_lean_nt(const AttnParams& p, int batch, int grid, hipStream_t s) {
+static void launch_lean_nt(const AttnParams& p, int batch, int grid, bool align, hipStream_t s) {
   const int wgs = grid + (p.two_pass ? 0 : batch * p.n_kv * ((p.R + 3) / 4));
   if constexpr (NT == 1 && !CS) {
     if (p.rot_cos) {  // a separate kernel: the rotary code costs the plain decode a few tenths of a us
-      if (batch <= 64)
-        decode_lean_kernel<NT, 1, CS, G, true><<<wgs, 256, 0, s>>>(p);
+      if (align)
+        batch <= 64 ? decode_lean_kernel<NT, 1, CS, G, true, true><<<wgs, 256, 0, s>>>(p)
+                    : decode_lean_kernel<NT, rows::kChunks, CS, G, true, true><<<wgs, 256, 0, s>>>(p);
       else
-        decode_lean_kernel<NT, rows::kChunks, CS, G, true><<<wgs, 256, 0, s>>>(p);
+        batch <= 64 ? decode_lean_kernel<NT, 1, CS, G, true><<<wgs, 256, 0, s>>>(p)
+                    : decode_lean_kernel<NT, rows::kChunks, CS, G, true><<<wgs, 256, 0, s>>>(p);
+      return;
+    }
+    if (align) {
+      batch <= 64 ? decode_lean_kernel<NT, 1, CS, G, false, true><<<wgs, 256, 0, s>>>(p)
+                  : decode_lean_kernel<NT, rows::kChunks, CS, G, false, true><<<wgs, 256, 0, s>>>(p);
       return;
     }
   }
@@ -3196,34 +3316,34 @@ static void launch_lean_nt(const AttnParams& p, int batch, int grid, hipStream_t
 // The launch (and the two-pass merge's) for geometry G; the suffix pass of a cascade launch
 // (cascade_splits > 0) exists for the 7B geometry only.
 template <typename G>
-static void launch_lean_g(const AttnParams& p, int R, int batch, int grid, hipStream_t s) {
+static void launch_lean_g(const AttnParams& p, int R, int batch, int grid, bool align, hipStream_t s) {
   const bool cs = p.cascade_splits > 0;
   if constexpr (std::is_same<G, Geom7B>::value) {
     switch ((R + 15) / 16) {
-      case 1: launch_lean_nt<1, false, G>(p, batch, grid, s); break;
-      case 2: cs ? launch_lean_nt<2, true, G>(p, batch, grid, s) : launch_lean_nt<2, false, G>(p, batch, grid, s); break;
-      case 3: cs ? launch_lean_nt<3, true, G>(p, batch, grid, s) : launch_lean_nt<3, false, G>(p, batch, grid, s); break;
-      default: cs ? launch_lean_nt<4, true, G>(p, batch, grid, s) : launch_lean_nt<4, false, G>(p, batch, grid, s); break;
+      case 1: launch_lean_nt<1, false, G>(p, batch, grid, align, s); break;
+      case 2: cs ? launch_lean_nt<2, true, G>(p, batch, grid, align, s) : launch_lean_nt<2, false, G>(p, batch, grid, align, s); break;
+      case 3: cs ? launch_lean_nt<3, true, G>(p, batch, grid, align, s) : launch_lean_nt<3, false, G>(p, batch, grid, align, s); break;
+      default: cs ? launch_lean_nt<4, true, G>(p, batch, grid, align, s) : launch_lean_nt<4, false, G>(p, batch, grid, align, s); break;
     }
   } else {
     (void)cs;
     switch ((R + 15) / 16) {
-      case 1: launch_lean_nt<1, false, G>(p, batch, grid, s); break;
-      case 2: launch_lean_nt<2, false, G>(p, batch, grid, s); break;
-      case 3: launch_lean_nt<3, false, G>(p, batch, grid, s); break;
-      default: launch_lean_nt<4, false, G>(p, batch, grid, s); break;
+      case 1: launch_lean_nt<1, false, G>(p, batch, grid, align, s); break;
+      case 2: launch_lean_nt<2, false, G>(p, batch, grid, align, s); break;
+      case 3: launch_lean_nt<3, false, G>(p, batch, grid, align, s); break;
+      default: launch_lean_nt<4, false, G>(p, batch, grid, align, s); break;
     }
   }
   if (p.two_pass)
-    combine_lean_kernel<G><<<dim3(p.n_kv, batch, (R + 7) / 8), 64 * (R < 8 ? R : 8), 0, s>>>(p, grid);
+    combine_lean_kernel<G><<<dim3(p.n_kv, batch, (R + 7) / 8), 64 * (R < 8 ? R : 8), 0, s>>>(p, grid, align ? 1 : 0);
 }
-static void launch_lean(const AttnParams& p, int head_dim, int R, int batch, int grid, hipStream_t s) {
+static void launch_lean(const AttnParams& p, int head_dim, int R, int batch, int grid, bool align, hipStream_t s) {
   switch (lean_geom(head_dim, p.n_kv)) {
-    case kGeom128x4: launch_lean_g<Geom<128, 4>>(p, R, batch, grid, s); break;
-    case kGeom128x2: launch_lean_g<Geom<128, 2>>(p, R, batch, grid, s); break;
-    case kGeom128x1: launch_lean_g<Geom<128, 1>>(p, R, batch, grid, s); break;
-    case kGeom64x4: launch_lean_g<Geom<64, 4>>(p, R, batch, grid, s); break;
-    case kGeom64x2: launch_lean_g<Geom<64, 2>>(p, R, batch, grid, s); break;
+    case kGeom128x4: launch_lean_g<Geom<128, 4>>(p, R, batch, grid, align, s); break;
+    case kGeom128x2: launch_lean_g<Geom<128, 2>>(p, R, batch, grid, align, s); break;
+    case kGeom128x1: launch_lean_g<Geom<128, 1>>(p, R, batch, grid, align, s); break;
+    case kGeom64x4: launch_lean_g<Geom<64, 4>>(p, R, batch, grid, align, s); break;
+    case kGeom64x2: launch_lean_g<Geom<64, 2>>(p, R, batch, grid, align, s); break;
     default: break;
   }
 }
@@ -3555,10 +3675,20 @@ static int decode_attn(const char* fn, bool use_scratch, const void* q, int64_t 
     while (p.cnt_stride < 32 && n_cnt * p.cnt_stride * 2 <= kMaxCounters) p.cnt_stride *= 2;
     p.lean_grid = grid;
     p.n_groups = n_kv / lean_heads_per_group(head_dim, n_kv);
+    // The sequence-aligned split (aligned_range; used where its ranges fit the grid) for decode
+    // rows of several sequences where a range crossing a sequence costs most: geometries with
+    // phase waves (fewer than 4 KV heads per group: a segment end merges the phases through LDS)
+    // and batches of up to 8 (ranges of a few tiles).  Interleaved on one box, per call: 7B at
+    // B = 8 14.9 against 16.1 us, 0.5B at B = 32 14.0 against 15.2-15.4, 7B TP-4 15.0 against
+    // 17.6; its prologue made 7B at B = 1, 16 and 32 0.3-0.4 us slower.  Not for 4 KV heads of
+    // head_dim 64, whose aligned instantiation compiles to a tile loop with 3x the scalar spills.
+    const int geom = lean_geom(head_dim, n_kv);
+    const bool align = R <= 16 && batch >= 2 && geom != kGeom64x4 &&
+                       (lean_heads_per_group(head_dim, n_kv) < 4 || batch <= 8);
     p.tok_elems = n_kv * head_dim;
     // every balanced launch writes split-K partials and counters: never launch one without them
     if (!p.ws_cnt || !p.ws_o || !p.ws_ml) return fail(PKV_EINVAL, "%s: balanced launch without a workspace", fn);
-    launch_lean(p, head_dim, R, batch, grid, s);
+    launch_lean(p, head_dim, R, batch, grid, align, s);
     return check_launch(fn);
   }
 
@@ -3730,7 +3860,7 @@ extern "C" int pkv_cascade_attn(const void* q, int64_t q_sb, int64_t q_ss, int64
   constexpr int NT = PKV_PREFILL_LDS_NT, W = PKV_PREFILL_LDS_W;
   const dim3 pgrid((batch * R + 16 * NT * W - 1) / (16 * NT * W), rows::NKV, S);
   prefill_lds_kernel<NT, W, PKV_PREFILL_LDS_NBUF, PKV_PREFILL_LDS_SUB, true><<<pgrid, 64 * W, 0, s>>>(p);
-  launch_lean_g<Geom7B>(p, R, batch, grid, s);  // suffix pass + the merge of every part (two_pass)
+  launch_lean_g<Geom7B>(p, R, batch, grid, false, s);  // suffix pass + the merge of every part (two_pass)
   return check_launch(fn);
 }
 

@@ -245,6 +245,34 @@ def test_balanced_kernel_narrow_geometries(gpu, case, merge):
                    what=f"geom{case[:1] + case[2:]}-{merge}")
 
 
+# The sequence-aligned split (decode rows of 2-8 sequences at 4 KV heads per group, any batch with
+# phase waves): per = ceil(T / grid) tiles per range, ceil(t_b / per) ranges per sequence when they
+# fit the grid, else the plain split.  After a 1-row append the 7B cases hold t = [3, 2, 1, 4]
+# tiles: grid 6 fits exactly (per 2: 2 + 1 + 1 + 2 ranges), grid 5 misses by one (plain split),
+# grid 8 leaves two workgroups idle; eight 2048-key sequences fill all 256 ranges of two tiles
+# (every sequence a whole number of ranges).
+ALIGNED_CASES = [
+    # (batch, ctx, n_kv, n_heads, hd, grid)
+    (4, [95, 63, 30, 126], 4, 28, 128, 6),
+    (4, [95, 63, 30, 126], 4, 28, 128, 5),
+    (4, [95, 63, 30, 126], 4, 28, 128, 8),
+    (8, [2047] * 8, 4, 28, 128, 0),
+    (7, [3000, 17, 4100, 800, 1, 2500, 64], 4, 28, 128, 0),
+    (5, [10, 2000, 130, 40, 250], 1, 7, 128, 0),               # 7B, TP 4 (4 phase waves)
+    (12, [(i * 311) % 1500 for i in range(12)], 2, 14, 64, 0),  # 0.5B (2 phase waves)
+    (3, [127, 128, 129], 2, 14, 128, 4),                        # 7B, TP 2
+]
+
+
+@pytest.mark.parametrize("merge", ["two-pass", "in-launch"])
+@pytest.mark.parametrize("case", ALIGNED_CASES, ids=[f"a{i}" for i in range(len(ALIGNED_CASES))])
+def test_sequence_aligned_split(gpu, case, merge):
+    B, ctx, n_kv, nh, hd, grid = case
+    _run_and_check(gpu, batch=B, ctx=ctx, page_size=256, n_kv=n_kv, n_heads=nh, head_dim=hd, s_q=1,
+                   grid=grid, two_pass=merge == "two-pass", seed=B + grid + n_kv,
+                   what=f"aligned{case}-{merge}")
+
+
 def test_balanced_in_launch_merge_rearms_across_calls(gpu):
     # the balanced kernel's per-(sequence, head) arrival counters must be back at zero after every
     # call: consecutive calls of different shapes and grids share one workspace, with sequences
