@@ -1868,7 +1868,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 // launch, by workgroups on any XCD).
 // BIG: parts per round trip beyond the first 8 (64: up to 16 loads in flight per lane; the
 // combine launch takes 32, for a register count at which several of its workgroups share a CU:
-// config-5 verify's combine 9.9 -> 7.9 us, its cascade merge 13.5 -> 9.2 us).
+// config-5 verify's combine 9.9 -> 7.9 us, its cascade merge 13.5 -> 9.2 us; 128 for a single
+// sequence's parts, lane u then loading the log-sum-exps of parts u and u + 64).
 template <typename G, bool COH, int NR, int BIG, typename RowOf>
 __device__ __forceinline__ void merge_rows(const AttnParams& p, int hk, int b, const int (&rr)[NR], int n_parts,
                                            RowOf row_of) {
@@ -1894,18 +1895,22 @@ __device__ __forceinline__ void merge_rows(const AttnParams& p, int hk, int b, c
   // the sums (rows with rr[q] < 0 are skipped)
   auto batch = [&](auto kp, int u0, int nb) {
     constexpr int KP = decltype(kp)::value;
-    float lse[NR];
+    constexpr int NL = (KP * PG + 63) / 64;  // log-sum-exps per lane: part u at lane u % 64, slot u / 64
+    float lse[NR][NL];
     u32x4 x[NR][KP];
 #pragma unroll
     for (int q = 0; q < NR; ++q) {
-      lse[q] = -INFINITY;
-      if (rr[q] >= 0 && lane < nb) {
-        const int64_t row = row_of(u0 + lane, rr[q]);
-        if constexpr (COH)
-          lse[q] = __builtin_bit_cast(
-              float, __builtin_amdgcn_raw_buffer_load_b32(rs, int(lse0 + uint32_t(row) * 4u), 0, kCoherent));
-        else
-          lse[q] = p.ws_ml[row];
+#pragma unroll
+      for (int l = 0; l < NL; ++l) {
+        lse[q][l] = -INFINITY;
+        if (rr[q] >= 0 && lane + 64 * l < nb) {
+          const int64_t row = row_of(u0 + lane + 64 * l, rr[q]);
+          if constexpr (COH)
+            lse[q][l] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(rs, int(lse0 + uint32_t(row) * 4u), 0, kCoherent));
+          else
+            lse[q][l] = p.ws_ml[row];
+        }
       }
 #pragma unroll
       for (int k = 0; k < KP; ++k) {
@@ -1922,17 +1927,26 @@ __device__ __forceinline__ void merge_rows(const AttnParams& p, int hk, int b, c
     }
 #pragma unroll
     for (int q = 0; q < NR; ++q) {
-      const float M_new = fmaxf(M_run[q], wave_max(lse[q]));
+      float lmax = lse[q][0];
+#pragma unroll
+      for (int l = 1; l < NL; ++l) lmax = fmaxf(lmax, lse[q][l]);
+      const float M_new = fmaxf(M_run[q], wave_max(lmax));
       const float M_use = (M_new == -INFINITY) ? 0.f : M_new;
-      const float w = fast_exp2(lse[q] - M_use);  // 0 for lanes past the batch
+      float w[NL], wsum = 0.f;
+#pragma unroll
+      for (int l = 0; l < NL; ++l) {
+        w[l] = fast_exp2(lse[q][l] - M_use);  // 0 for parts past the batch
+        wsum += w[l];
+      }
       const float resc = fast_exp2(M_run[q] - M_use);
-      S_run[q] = S_run[q] * resc + wave_sum(w);
+      S_run[q] = S_run[q] * resc + wave_sum(wsum);
       M_run[q] = M_new;
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[q][e] *= resc;
 #pragma unroll
       for (int k = 0; k < KP; ++k) {
-        const float wk = __shfl(w, PG * k + pg, 64);
+        // part PG k + pg: slot (PG k) / 64 for every pg (PG divides 64)
+        const float wk = __shfl(w[(PG * k) / 64], (PG * k + pg) & 63, 64);
         float f[8];
         unpack_f16x8(x[q][k], f);
 #pragma unroll
@@ -2019,7 +2033,7 @@ __device__ __forceinline__ int* merge_counter(const AttnParams& p, int gb, int h
   return p.ws_cnt + ((gb * G::HG + h) * n_rq + rq) * p.cnt_stride;
 }
 
-template <typename G, int NCH>
+template <typename G, int NCH, int MBIG>
 __device__ __forceinline__ void merge_workgroup(const AttnParams& p, const SeqTable<NCH>& st,
                                                 const RangeTable<NCH>& rt, bool aligned, int T1, int per,
                                                 int* ready_s) {
@@ -2064,7 +2078,7 @@ __device__ __forceinline__ void merge_workgroup(const AttnParams& p, const SeqTa
   const int r0 = 4 * rq + int(threadIdx.x >> 6);
   const int rr[1] = {r0 < p.R ? r0 : -1};
   if (*ready_s == 1 && rr[0] >= 0)
-    merge_rows<G, true, 1, 64>(p, hk, b, rr, sp.np, [&](int part, int r) -> int64_t {
+    merge_rows<G, true, 1, MBIG>(p, hk, b, rr, sp.np, [&](int part, int r) -> int64_t {
       const int slot = part == 0 ? sp.slot0 : 2 * (sp.w0 + part);
       return (int64_t(slot) * G::HG + h) * p.R + r;
     });
@@ -2140,9 +2154,13 @@ __device__ __forceinline__ void phase_merge(char* buf, float (&m_run)[NT], float
   }
 }
 
-template <int NT, int NCH, bool CASCADE_SUFFIX, typename G, bool ROPE = false, bool ALIGN = false>
+// MBIG: split-K parts the in-launch merge fetches per round trip (64; 128 in the instantiation for a
+// single sequence, whose parts number one per workgroup: a 2048-key call has 65, a 32767-key
+// call 256, and each further round trip is ~1 us on the launch's critical path).
+template <int NT, int NCH, bool CASCADE_SUFFIX, typename G, bool ROPE = false, bool ALIGN = false, int MBIG = 64>
 __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p) {
   static_assert(!ALIGN || (NT == 1 && !CASCADE_SUFFIX), "the aligned split is for decode rows");
+  static_assert(MBIG == 64 || (NT == 1 && !CASCADE_SUFFIX && !ALIGN), "wide merges are for one decode sequence");
   constexpr int HD = G::HD;
   constexpr int DPL = HD / 16;
   constexpr int KK = HD / 32;
@@ -2187,7 +2205,7 @@ __global__ __launch_bounds__(256, 1) void decode_lean_kernel(const AttnParams p)
     aligned = rt.rtotal * p.n_groups <= p.lean_grid;
   }
   if (int(blockIdx.x) >= p.lean_grid) {
-    if constexpr (NT == 1) merge_workgroup<G, NCH>(p, st, rt, aligned, T1, per, reinterpret_cast<int*>(lds));
+    if constexpr (NT == 1) merge_workgroup<G, NCH, MBIG>(p, st, rt, aligned, T1, per, reinterpret_cast<int*>(lds));
     return;
   }
   int s, e;
@@ -3306,6 +3324,14 @@ static void launch_lean_nt(const AttnParams& p, int batch, int grid, bool align,
       batch <= 64 ? decode_lean_kernel<NT, 1, CS, G, false, true><<<wgs, 256, 0, s>>>(p)
                   : decode_lean_kernel<NT, rows::kChunks, CS, G, false, true><<<wgs, 256, 0, s>>>(p);
       return;
+    }
+    // not for 1 or 2 KV heads of head_dim 128 per group, whose wide-merge instantiation compiles
+    // to a tile loop with 5-7x the scalar spills
+    if constexpr (!(G::HD == 128 && G::HG < 4)) {
+      if (batch == 1 && !p.two_pass) {
+        decode_lean_kernel<NT, 1, CS, G, false, false, 128><<<wgs, 256, 0, s>>>(p);
+        return;
+      }
     }
   }
   if (batch <= 64)
