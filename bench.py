@@ -68,7 +68,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=4, help="layers in the CPU baseline sample")
     ap.add_argument("--stamp-calls", type=int, default=10, help="stamped calls read by --workload tile-stamps")
-    ap.add_argument("--stamps-of", choices=["config3", "config2", "decode-0.5B", "decode-7B-tp4"], default="config3",
+    ap.add_argument("--stamps-of", choices=["config3", "config2", "config5", "decode-0.5B", "decode-7B-tp4"],
+                    default="config3",
                     help="the decode workload --workload tile-stamps records")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after timing, copy this many MiB of pages once (counter calibration)")
