@@ -73,6 +73,7 @@ def _decode(lib, **over):
     (dict(flags=1 << 30), "bad flags"),
     (dict(k=0), "both be given"),
     (dict(scale=0.0), "softmax_scale"),
+    (dict(max_blocks=(1 << 19) + 1, bt_stride=(1 << 19) + 1), "2^27 keys"),
     (dict(bt=0), "null"),
     (dict(num_pages=0), "bad sizes"),
     (dict(page_stride=100), "page stride"),
@@ -186,3 +187,25 @@ def test_noalloc_rejects_before_any_device_work(lib):
     assert _decode_noalloc(lib, **over) == _lib.PKV_ENOSPC
     err = lib.pkv_last_error().decode()
     assert "static scratch" in err and str(need) in err, err
+
+
+def test_stamps_library_is_the_same_abi_plus_its_readers():
+    """bench.py --workload tile-stamps swaps libprism_kv_stamps.so in for libprism_kv.so: it must
+    export every header function with the same ABI version, and its three stamp readers."""
+    from prism_amd.build import STAMPS_LIB_PATH
+
+    if not STAMPS_LIB_PATH.exists():
+        pytest.fail(f"{STAMPS_LIB_PATH} is not built (python -m prism_amd.build)")
+    slib = ctypes.CDLL(str(STAMPS_LIB_PATH))
+    for name in _lib.header_symbols():
+        assert hasattr(slib, name), f"{name} missing from the stamps build"
+    slib.pkv_abi_version.restype = ctypes.c_int32
+    assert slib.pkv_abi_version() == _lib.ABI_VERSION
+    for name in ("pkv_tile_stamps", "pkv_tile_stamps_clear", "pkv_tile_stamp_words"):
+        assert hasattr(slib, name), name
+    slib.pkv_tile_stamp_words.restype = ctypes.c_int
+    words = slib.pkv_tile_stamp_words()
+    assert words == 1024 * 32 + 4 * 4096
+    # too small a destination is rejected before any HIP call
+    slib.pkv_tile_stamps.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    assert slib.pkv_tile_stamps(ctypes.c_void_p(A16), 8, None) == _lib.PKV_EINVAL
