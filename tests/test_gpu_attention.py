@@ -261,6 +261,8 @@ ALIGNED_CASES = [
     (5, [10, 2000, 130, 40, 250], 1, 7, 128, 0),               # 7B, TP 4 (4 phase waves)
     (12, [(i * 311) % 1500 for i in range(12)], 2, 14, 64, 0),  # 0.5B (2 phase waves)
     (3, [127, 128, 129], 2, 14, 128, 4),                        # 7B, TP 2
+    (70, [(i * 53) % 900 for i in range(70)], 2, 14, 64, 0),   # 0.5B past 64 sequences (4-chunk scan)
+    (70, [(i * 53) % 900 for i in range(70)], 1, 7, 128, 0),   # TP 4 past 64 sequences
 ]
 
 
