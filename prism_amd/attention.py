@@ -37,6 +37,11 @@ _captured: set[int] = set()         # data_ptr of every workspace handed to a ca
 _retired: list[torch.Tensor] = []   # outgrown workspaces a captured graph may still use
 _status: dict[int, torch.Tensor] = {}
 _STATUS_NAMES = {1: "BAD_PAGE", 2: "BAD_POSITION", 4: "SHARED_PREFIX", 8: "PARTIAL_RANGE", 16: "MERGE_TIMEOUT"}
+# The split-K workspace's leading counter region (kCounterBytes in prism_amd/csrc/pkv_attention.hip:
+# 16384 int32 arrival counters), then the balanced kernel's partial rows: per workgroup two slots of
+# at most 4 KV heads x R rows x (128 fp16 + one fp32 log-sum-exp) = 260 bytes per row.
+_COUNTER_BYTES = 65536
+_LEAN_ROW_BYTES = 260
 
 
 def _stream_ptr(device: torch.device) -> int:
@@ -137,7 +142,7 @@ def _recover(idx: int, bits: int) -> None:
     with _ws_lock:
         for (d, _), ws in _workspaces.items():
             if d == idx:
-                ws[:65536].zero_()
+                ws[:_COUNTER_BYTES].zero_()
     _reset_counters.add(idx)
 
 
@@ -476,7 +481,7 @@ def flash_attn_with_kvcache(
         nbytes = lib.pkv_decode_workspace_bytes(batch, s_q, n_heads, n_kv, hd, page_size, max_blocks,
                                                 int(split_tokens))
         if grid:  # the balanced kernel's partials for `grid` workgroups (prism_kv.h's bound)
-            nbytes = max(nbytes, 65536 + 2 * int(grid) * 4 * s_q * g * 260)
+            nbytes = max(nbytes, _COUNTER_BYTES + 2 * int(grid) * 4 * s_q * g * _LEAN_ROW_BYTES)
         ws = None if noalloc else _workspace(device, nbytes, stream, allow_static=True)
         if noalloc or (ws is None and nbytes > 0):
             idx = _dev_index(device)
@@ -580,7 +585,7 @@ def rope_decode_attention(qkv: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     stream = _stream_ptr(device)
     nbytes = lib.pkv_decode_workspace_bytes(batch, s_q, n_heads, n_kv, hd, page_size, max_blocks, 0)
     if grid:
-        nbytes = max(nbytes, 65536 + 2 * int(grid) * 4 * s_q * (n_heads // n_kv) * 260)
+        nbytes = max(nbytes, _COUNTER_BYTES + 2 * int(grid) * 4 * s_q * (n_heads // n_kv) * _LEAN_ROW_BYTES)
     ws = _workspace(device, nbytes, stream)
     rc = lib.pkv_decode_attn_rope(
         q.data_ptr(), *qs, k.data_ptr(), *ks, v.data_ptr(), *vs,
