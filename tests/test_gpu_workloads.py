@@ -14,7 +14,8 @@ pools, block tables and lengths bench.py times, and is checked against the CPU o
 
 The oracle sees only the pages the batch references (gathered on the device, block tables remapped
 onto them), so an fp64 check of a full-size layer takes about a second.  Config 4's prefill
-oracle runs on a sample of two KV heads (10 query heads); its append check covers every head.
+oracle runs on two KV heads (10 query heads) at every row of one layer and on every head at a
+sample of rows of another; its append check covers every head.
 """
 from __future__ import annotations
 
@@ -115,15 +116,20 @@ def test_ragged_decode_other_shapes(gpu, shape):
 
 def test_config4_chunked_prefill(gpu):
     # 14B: 8 chunks of 512 appended onto prefixes ~U{0..4096}, causal within the chunk; the fp64
-    # oracle on KV heads 0 and 5 (query heads 0-4 and 25-29) of every sequence and row
+    # oracle on KV heads 0 and 5 (query heads 0-4 and 25-29) of every sequence and row at layer 0,
+    # and on all 40 query heads at a sample of 64 query rows (tile and chunk edges included) at
+    # layer 47
     w = workloads.config4(gpu, seed=0)
     assert w.layers == 48 and w.s_q == 512 and w.batch == 8
-    for l in (0, 47):
+    edges = [0, 1, 15, 16, 31, 32, 33, 127, 128, 255, 256, 257, 383, 384, 510, 511]
+    draw = np.random.default_rng(4).choice(512, size=48, replace=False)
+    rows47 = np.unique(np.concatenate([edges, draw]))
+    for l, heads, rows in ((0, [0, 5], None), (47, None, rows47)):
         print(f"config4 layer {l}: prefixes {w.ctx.tolist()}", flush=True)
-        chk = LayerCheck(w, l, kv_heads=[0, 5])
+        chk = LayerCheck(w, l, kv_heads=heads)
         out = torch.full_like(w.q[l], float("nan"))
         _call(w, l, out)
-        chk.check(out, f"config4 layer {l}")
+        chk.check(out, f"config4 layer {l}", rows=rows)
         assert torch.isfinite(out.float()).all(), "config4: a query head outside the sample was not written"
         del chk
         _free()
