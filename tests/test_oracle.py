@@ -235,3 +235,57 @@ def test_page_ops_copy_and_compact():
         assert (packed[i][3:] == 0).all()
     t = page_ops.transfer_sequence(pools, dst, [4, 1, 6], [2, 3, 5], seq_len=5, page_size=4)
     assert (t[0][2] == pools[0][4]).all() and (t[0][3] == pools[0][1]).all() and (t[0][5] == 0).all()
+
+
+# ----------------------------------------------------------------------------- rounding edge
+
+
+def _bf16_round(x):
+    """fp32 -> nearest-even bf16, returned as float64."""
+    return torch.from_numpy(np.asarray(x, np.float32)).to(torch.bfloat16).double().numpy()
+
+
+@pytest.mark.parametrize("seed,seq,expect", [(5283, 26, 0.0106), (5856, 8, 0.0100)])
+def test_bf16_p_rounding_reaches_the_tolerance_edge(seed, seq, expect):
+    """flash_attn's own rounding (P rounded to bf16 for the PV product, row sum from the unrounded
+    P, output rounded to bf16) lands at 1e-2 from the fp64 oracle on rows that see 2-4 keys: the
+    P rounding moves the row's value by ~0.003, across a bf16 rounding boundary of the output
+    (ulp 2^-6 for |o| in [2, 4)).  The two cases are random-case draws (seeds of
+    tests/test_gpu_random_cases.py's draw) whose speculative-verify rows the GPU kernel returns
+    with max-abs 0.0106 and 0.0100, the values this model gives; with P unrounded the same rows
+    stay within half an output ulp (0.0078)."""
+    from pkv_testutil import make_paged_case
+    from test_gpu_random_cases import draw
+    c = draw(seed)
+    cpu, _ = make_paged_case(torch.device("cpu"), batch=c["batch"], ctx=c["ctx"], page_size=c["page_size"],
+                             n_kv=c["n_kv"], n_heads=c["n_heads"], head_dim=c["head_dim"], s_q=c["s_q"], seed=seed)
+    kb, vb = pa.bf16_bits(cpu["k_cache"]), pa.bf16_bits(cpu["v_cache"])
+    bt = cpu["block_table"].numpy().astype(np.int64)
+    sl = cpu["cache_seqlens"].numpy().astype(np.int64)
+    if c["append"]:
+        kb, vb = pa.append_kv(kb, vb, pa.bf16_bits(cpu["k"]), pa.bf16_bits(cpu["v"]), bt, sl)
+        sl = sl + c["s_q"]
+    one = slice(seq, seq + 1)
+    ref = pa.attention_fp64(pa.bf16_bits(cpu["q"])[one], kb, vb, bt[one], sl[one], c["causal"], None)[0]
+    s_q, nh, hd, P = c["s_q"], c["n_heads"], c["head_dim"], c["page_size"]
+    L, g = int(sl[seq]), nh // c["n_kv"]
+    assert L < 8, "the case is a sequence with a handful of keys"
+    slots = bt[seq, np.arange(L) // P] * P + np.arange(L) % P
+    K, V = (torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).double().numpy().reshape(-1, c["n_kv"], hd)
+            for x in (kb, vb))
+    q = cpu["q"].double().numpy()[seq]
+    err_p, err_exact = 0.0, 0.0
+    for i in range(s_q):
+        vis = L - s_q + i + 1
+        if vis <= 0:
+            continue
+        for h in range(nh):
+            s = K[slots[:vis], h // g] @ q[i, h] / math.sqrt(hd)
+            p = np.exp(s - s.max()).astype(np.float32).astype(np.float64)
+            pv = V[slots[:vis], h // g]
+            o_p = _bf16_round((_bf16_round(p)[:, None] * pv).sum(0) / p.sum())
+            o_exact = _bf16_round((p[:, None] * pv).sum(0) / p.sum())
+            err_p = max(err_p, float(np.abs(o_p - ref[i, h]).max()))
+            err_exact = max(err_exact, float(np.abs(o_exact - ref[i, h]).max()))
+    assert err_p == pytest.approx(expect, abs=1e-4)
+    assert err_exact <= 2.0 ** -7
