@@ -8,7 +8,9 @@ balanced kernel for decode (R = 7) and verify (R = 35), with its two-pass and in
 and the per-head kernel with several splits per sequence (its in-launch merge counts arrivals in
 the array).  A call needing more scratch than the array holds is rejected before anything runs.
 Through the drop-in, a forked-branch table that would send the default call to cascade attention
-(which needs the module's workspace) runs the allocation-free path and allocates nothing.
+(which needs the module's workspace) runs the allocation-free path and allocates nothing.  A
+fresh process whose first allocation-free call is made under graph capture (the scratch lookup and
+its counter clearing then happen inside the capture) replays to the eager call's output.
 """
 
 import pytest
@@ -195,3 +197,53 @@ def test_noalloc_inside_a_captured_graph(gpu):
                                                causal=True)
     assert_attn_close(out, exp, "noalloc captured verify")
     assert prism_amd.read_status(gpu) == 0
+
+
+_FIRST_CALL_CAPTURED = r"""
+import sys, torch
+sys.path[:0] = [{repo!r}, {tests!r}]
+import numpy as np, prism_amd
+from oracle import paged_attention as pa
+from pkv_testutil import attn_errors, make_paged_case
+gpu = torch.device("cuda:0")
+cpu, d = make_paged_case(gpu, batch=16, ctx=[(i * 397) % 3000 + 1 for i in range(16)], page_size=256, n_kv=4,
+                         n_heads=28, head_dim=128, s_q=1, seed=31)
+kw = dict(cache_seqlens=d["cache_seqlens"], block_table=d["block_table"], causal=True, noalloc=True)
+out = torch.full_like(d["q"], float("nan"))
+torch.cuda.synchronize()
+print("capturing the process's first noalloc call", flush=True)
+cap = torch.cuda.Stream(device=gpu)
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.stream(cap):
+    with torch.cuda.graph(graph, stream=cap):
+        prism_amd.flash_attn_with_kvcache(d["q"], d["k_cache"], d["v_cache"], out=out, **kw)
+torch.cuda.current_stream(gpu).wait_stream(cap)
+exp, _, _ = pa.flash_attn_with_kvcache_ref(cpu["q"], cpu["k_cache"], cpu["v_cache"],
+                                           cache_seqlens=cpu["cache_seqlens"], block_table=cpu["block_table"],
+                                           causal=True)
+first = None
+for rep in range(3):
+    out.fill_(float("nan"))
+    graph.replay()
+    eager = prism_amd.flash_attn_with_kvcache(d["q"], d["k_cache"], d["v_cache"], **kw)
+    torch.cuda.synchronize()
+    mx, mean = attn_errors(out, exp)
+    print(f"replay {{rep}}: max-abs {{mx:.3g}} mean-abs {{mean:.3g}}", flush=True)
+    assert mx <= 1e-2 and mean <= 1e-3
+    assert torch.equal(out, eager), "replay differs from the eager call"
+assert prism_amd.read_status(gpu) == 0
+print("ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture():
+    # a fresh process whose first noalloc call is made under graph capture: the scratch lookup and
+    # its counter clearing (a kernel recorded into the graph) happen inside the capture
+    import os
+    import subprocess
+    import sys
+    tests = os.path.dirname(os.path.abspath(__file__))
+    script = _FIRST_CALL_CAPTURED.format(repo=os.path.dirname(tests), tests=tests)
+    r = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=300)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and r.stdout.rstrip().endswith("ok")
